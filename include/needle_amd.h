@@ -1,0 +1,155 @@
+/*
+ * needle_amd.h -- C ABI of the MI355X (gfx950) paged-KV hot path.
+ *
+ * Three operations replace the torch statement sequences of Needle's
+ * needle/layers/attention.py:
+ *
+ *   ndl_kv_append       scatter new K/V rows into the block pool
+ *                       (decode append attention.py:141-154, _write_kv :204-246)
+ *   ndl_paged_decode    one-query-per-sequence attention over block_table
+ *                       (_decode_pytorch :291-310, dispatched from _decode :156-159;
+ *                        also covers the FlashInfer wrapper :161-197)
+ *   ndl_varlen_prefill  causal attention of packed varlen prompts, reading K/V
+ *                       back through block_table
+ *                       (_prefill_pytorch :120-134; FlashInfer path :109-118)
+ *
+ * Conventions (every entry point):
+ *   - Plain pointers to device memory, element counts and strides in ELEMENTS.
+ *   - KV pool layout (needle/model/runner.py:65-78, attention.py:9-10):
+ *       kv_cache[2][num_blocks][num_kv_heads][block_size][head_dim],
+ *       plane 0 = K, plane 1 = V, both contiguous.
+ *   - block_table is int32 [num_seqs][bt_row_stride], the first
+ *     max_blocks_per_seq entries of each row are meaningful (runner.py:220-235).
+ *   - context_lens[i] = tokens already in the cache before this call
+ *     (runner.py:204-218).
+ *   - Work is enqueued on `stream`; nothing synchronises with the host and
+ *     nothing is allocated.  Scratch memory is passed in by the caller.
+ *   - Return 0 on success or a negative NDL_ERR_* code.  Never aborts.
+ *   - Block ids outside [0, num_blocks) are never dereferenced: append skips
+ *     such rows and attention treats such blocks as empty (the reference
+ *     raises an indexing error there instead).
+ */
+#ifndef NEEDLE_AMD_H
+#define NEEDLE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Same object as hipStream_t; declared here so callers need no HIP headers. */
+typedef struct ihipStream_t* ndl_stream_t;
+
+#define NDL_ABI_VERSION 1
+
+enum ndl_status {
+  NDL_OK = 0,
+  NDL_ERR_INVALID_ARG = -1,   /* null pointer, negative size, inconsistent shape */
+  NDL_ERR_UNSUPPORTED = -2,   /* dtype / head_dim / block_size / group size not built */
+  NDL_ERR_WORKSPACE = -3,     /* workspace smaller than the *_workspace_bytes query */
+  NDL_ERR_LAUNCH = -4         /* the HIP runtime rejected a kernel launch */
+};
+
+enum ndl_dtype {
+  NDL_DTYPE_BF16 = 0,
+  NDL_DTYPE_F16 = 1
+};
+
+/* ABI version of the loaded library (NDL_ABI_VERSION at build time). */
+int ndl_abi_version(void);
+
+/* Static, human-readable text for a status code. */
+const char* ndl_strerror(int status);
+
+/*
+ * Scatter-append K/V rows into the paged pool.
+ *
+ * Replaces: needle/layers/attention.py:141-154 (decode: one token per sequence)
+ *           needle/layers/attention.py:204-246 (_write_kv: packed varlen tokens)
+ *
+ * Token t of sequence i (cu_seqlens[i] <= t < cu_seqlens[i+1]) is written to
+ *   p   = context_lens[i] + (t - cu_seqlens[i])
+ *   col = min(p / block_size, max_blocks_per_seq - 1)       (attention.py:144,235)
+ *   blk = block_table[i * bt_row_stride + col]               (attention.py:145,236)
+ *   kv_cache[0][blk][h][p % block_size][:] = k[t][h][:]      (attention.py:153,245)
+ *   kv_cache[1][blk][h][p % block_size][:] = v[t][h][:]      (attention.py:154,246)
+ * for every kv head h.  cu_seqlens == NULL means one token per sequence
+ * (t == i, num_tokens == num_seqs), which is the decode form.
+ *
+ * k, v: [num_tokens][num_kv_heads][head_dim], token stride k_tok_stride /
+ * v_tok_stride elements, rows inside a token contiguous.  The copy is
+ * bit-exact.  Any head_dim that is a multiple of 8 is accepted.
+ */
+int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int block_size,
+                  int head_dim, int dtype,
+                  const void* k, int64_t k_tok_stride,
+                  const void* v, int64_t v_tok_stride,
+                  const int32_t* block_table, int64_t bt_row_stride, int max_blocks_per_seq,
+                  const int32_t* cu_seqlens, const int32_t* context_lens,
+                  int num_seqs, int64_t num_tokens, ndl_stream_t stream);
+
+/*
+ * Bytes of scratch ndl_paged_decode needs for this shape.  partition_tokens
+ * = 0 selects the built-in default; pass the same value to ndl_paged_decode.
+ */
+size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
+                                        int max_blocks_per_seq, int block_size,
+                                        int partition_tokens);
+
+/*
+ * Paged decode attention, one query token per sequence.
+ *
+ * Replaces: needle/layers/attention.py:291-310 (_decode_pytorch) and the
+ *           FlashInfer decode wrapper :161-197.
+ *
+ * For sequence i, L_i = min(context_lens[i] + 1, max_blocks_per_seq * block_size)
+ * tokens are attended (attention.py:299-303: the token appended by this step is
+ * included; a row of the table never yields more than its width).  Query head h
+ * reads kv head h / (num_heads / num_kv_heads) (attention.py:304-306).
+ *   out[i][h][:] = softmax(scale * q[i][h] . K_i^T) V_i            (:307-308)
+ * q: [num_seqs][num_heads][head_dim], token stride q_tok_stride.
+ * out: [num_seqs][num_heads][head_dim] contiguous.  fp32 accumulation.
+ * L_i <= 0 gives zeros.  Supported: bf16, block_size 16, head_dim 64 or 128,
+ * num_heads / num_kv_heads in 1..16.
+ */
+int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
+                     const void* kv_cache, int64_t num_blocks,
+                     const int32_t* block_table, int64_t bt_row_stride, int max_blocks_per_seq,
+                     const int32_t* context_lens, int num_seqs,
+                     int num_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
+                     float scale, int partition_tokens,
+                     void* workspace, size_t workspace_bytes, ndl_stream_t stream);
+
+/*
+ * Varlen causal prefill attention over the paged cache.
+ *
+ * Replaces: needle/layers/attention.py:120-134 (_prefill_pytorch) and the
+ *           FlashInfer prefill path :109-118.
+ *
+ * Query token t of sequence i sits at position p = context_lens[i] + (t - cu_seqlens[i])
+ * and attends cache positions 0..p of sequence i, read through block_table
+ * with the same column clamp as ndl_kv_append.  K/V of the new tokens must
+ * already be in the cache (call ndl_kv_append first, as _prefill does at
+ * attention.py:103).  With context_lens == 0 this is exactly the
+ * reference's per-sequence causal SDPA (attention.py:132); with
+ * context_lens > 0 the cached prefix is attended as well.
+ * q: [num_tokens][num_heads][head_dim], token stride q_tok_stride.
+ * out: [num_tokens][num_heads][head_dim] contiguous.
+ * max_seqlen: host-known bound on cu_seqlens[i+1] - cu_seqlens[i].
+ * max_context_len: host-known bound on context_lens[i] (0 for plain prefill).
+ */
+int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
+                       const void* kv_cache, int64_t num_blocks,
+                       const int32_t* block_table, int64_t bt_row_stride, int max_blocks_per_seq,
+                       const int32_t* cu_seqlens, const int32_t* context_lens,
+                       int num_seqs, int64_t num_tokens, int max_seqlen, int max_context_len,
+                       int num_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
+                       float scale, ndl_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NEEDLE_AMD_H */

@@ -1,0 +1,361 @@
+// Paged decode attention for gfx950 (CDNA4).
+//
+// Reference: needle/layers/attention.py:291-310 (_decode_pytorch): per
+// sequence gather K/V blocks, expand the GQA group, softmax(q K^T * scale) V.
+//
+// Design (one wave64 per (sequence, kv head, context partition)):
+//   * The g query heads of a kv head are the N columns (padded to 16) of a
+//     16x16 MFMA tile; the 16 tokens of one cache block are its M rows.
+//     S^T = K . Q^T runs as head_dim/32 v_mfma_f32_16x16x32_bf16 steps whose
+//     A operand is read straight from the block (lane = token row, 16 bytes
+//     of head_dim per lane) -- no LDS, no conversion.
+//   * The S^T accumulator layout (lane 16j+c holds tokens 4j..4j+3 of head c)
+//     is exactly the B operand layout of v_mfma_f32_16x16x16bf16_1k, so
+//     P^T feeds O^T = V^T . P^T without any cross-lane movement.  V^T is the
+//     A operand; the head_dim index of the M rows is permuted (row m of
+//     m-block b is d = (D/16)*m + b) so that every lane loads D/16 contiguous
+//     elements of a V row and only repacks registers.
+//   * Online softmax in fp32 with exp2 (scale folded with log2 e).  The row
+//     max needs two cross-lane exchanges per block.
+//   * Long contexts split into partitions of `part_tokens`; partials
+//     (m, l, unnormalised acc) go to the workspace and a second kernel
+//     merges them.  A sequence that fits one partition is written directly.
+#include "ndl_common.hpp"
+
+namespace ndl {
+
+constexpr int kDecodeDefaultPartition = 256;
+constexpr int kDecodeMaxPartition = 1024;  // 64 blocks: one table entry per lane
+
+template <int D> struct VRow;
+template <> struct VRow<128> { using T = u32x4; };  // 8 bf16 per lane per token
+template <> struct VRow<64> { using T = u32x2; };   // 4 bf16 per lane per token
+
+template <int D>
+__device__ __forceinline__ typename VRow<D>::T load_vrow(const u16* p) {
+  if constexpr (D == 128) return ld16(p); else return ld8(p);
+}
+
+// Element e (0..D/16-1) of the per-lane V row chunk, as raw bf16 bits in the low half.
+template <int D>
+__device__ __forceinline__ uint32_t vrow_elem(const typename VRow<D>::T& r, int e) {
+  const uint32_t w = r[e >> 1];
+  return (e & 1) ? (w >> 16) : (w & 0xffffu);
+}
+
+struct DecodeArgs {
+  u16* out;
+  const u16* q;
+  int64_t q_tok_stride;
+  const u16* kplane;
+  const u16* vplane;
+  int64_t num_blocks;
+  int num_kv_heads;
+  const int32_t* block_table;
+  int64_t bt_row_stride;
+  int max_blocks;
+  const int32_t* context_lens;
+  int num_heads;
+  int group;
+  float scale_log2;
+  int part_tokens;
+  int max_parts;
+  float* ws_ml;   // [seq][head][part][2] = (m, l)
+  float* ws_acc;  // [seq][head][part][D]
+};
+
+__device__ __forceinline__ int64_t attended_len(const DecodeArgs& a, int seq) {
+  int64_t L = (int64_t)a.context_lens[seq] + 1;  // attention.py:299
+  const int64_t cap = (int64_t)a.max_blocks * 16;  // a table row holds at most W blocks
+  return L < cap ? L : cap;
+}
+
+template <int D>
+__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
+  constexpr int KS = D / 32;   // k-steps of the QK^T MFMA
+  constexpr int DPL = D / 16;  // head_dim elements per lane per V row
+  using VT = typename VRow<D>::T;
+
+  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  const int lane = threadIdx.x, j = lane >> 4, c = lane & 15;
+  const int64_t L = attended_len(a, seq);
+  const int nparts = L <= 0 ? 1 : (int)((L + a.part_tokens - 1) / a.part_tokens);
+  if (part >= nparts) return;
+  const bool head_ok = c < a.group;
+  const int head = kvh * a.group + c;
+  u16* const out_row = a.out + ((int64_t)seq * a.num_heads + head) * D + DPL * 4 * j;
+
+  if (L <= 0) {  // nothing to attend: zeros (attention.py:307-308 on an empty context)
+    if (head_ok) {
+#pragma unroll
+      for (int i = 0; i < 4 * DPL / 2; ++i) reinterpret_cast<uint32_t*>(out_row)[i] = 0u;
+    }
+    return;
+  }
+
+  const int t0 = part * a.part_tokens;
+  const int t1 = (int)(t0 + a.part_tokens < L ? t0 + a.part_tokens : L);
+  const int tile0 = t0 >> 4;
+  const int ntiles = (t1 - t0 + 15) >> 4;
+
+  // B operand of S^T = K Q^T: lane (j, c) supplies Q[head c][32 s + 8 j .. +8).
+  bf16x8 qb[KS];
+  {
+    const u16* qrow = a.q + (int64_t)seq * a.q_tok_stride + (int64_t)head * D + 8 * j;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 w = head_ok ? ld16(qrow + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+      qb[s] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+
+  // Block ids of this partition, one per lane (ntiles <= 64).
+  int bt_lane = 0;
+  if (lane < ntiles) bt_lane = a.block_table[(int64_t)seq * a.bt_row_stride + tile0 + lane];
+
+  const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
+  const int64_t head_off = (int64_t)kvh * 16 * D;
+  const int k_off = c * D + 8 * j;        // token row c, head_dim chunk j (+32 s)
+  const int v_off = 4 * j * D + DPL * c;  // token rows 4j..4j+3, head_dim DPL*c..
+
+  f32x4 acc[DPL];
+#pragma unroll
+  for (int b = 0; b < DPL; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m = kNegInf, lsum = 0.f;
+
+  for (int it = 0; it < ntiles; ++it) {
+    int64_t blk = __builtin_amdgcn_readlane(bt_lane, it);
+    const bool bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
+    if (bad) blk = 0;
+    const u16* kb = a.kplane + blk * blk_stride + head_off;
+    const u16* vb = a.vplane + blk * blk_stride + head_off;
+
+    u32x4 kr[KS];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) kr[s] = ld16(kb + k_off + 32 * s);
+    VT vr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) vr[i] = load_vrow<D>(vb + v_off + i * D);
+
+    f32x4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < KS; ++s)
+      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[s]), qb[s], st,
+                                                   0, 0, 0);
+
+    // st[i] is the score of token (tile0+it)*16 + 4j + i for head c.
+    const int pos0 = (tile0 + it) * 16 + 4 * j;
+    const bool partial = bad || ((tile0 + it) * 16 + 16 > t1);  // wave-uniform
+    float sc[4];
+    float mt = kNegInf;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool ok = !partial || (!bad && pos0 + i < t1);
+      sc[i] = ok ? st[i] * a.scale_log2 : kNegInf;
+      mt = fmaxf(mt, sc[i]);
+    }
+    mt = fmaxf(mt, xor_shfl(mt, 16));
+    mt = fmaxf(mt, xor_shfl(mt, 32));
+    const float m_new = fmaxf(m, mt);
+    const float m_use = m_new == kNegInf ? 0.f : m_new;
+    const float alpha = fast_exp2(m - m_use);
+    float p[4];
+    float ps = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      p[i] = fast_exp2(sc[i] - m_use);
+      ps += p[i];
+    }
+    lsum = lsum * alpha + ps;
+    m = m_new;
+#pragma unroll
+    for (int b = 0; b < DPL; ++b) acc[b] *= alpha;
+
+    if (partial) {  // masked rows may hold stale bits (NaN * 0 = NaN): clear them
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = !bad && pos0 + i < t1;
+        if (!ok) vr[i] = VT{};
+      }
+    }
+
+    const i16x4 pb = __builtin_bit_cast(
+        i16x4, u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])});
+#pragma unroll
+    for (int b = 0; b < DPL; ++b) {
+      const uint32_t w01 = vrow_elem<D>(vr[0], b) | (vrow_elem<D>(vr[1], b) << 16);
+      const uint32_t w23 = vrow_elem<D>(vr[2], b) | (vrow_elem<D>(vr[3], b) << 16);
+      acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+          __builtin_bit_cast(i16x4, u32x2{w01, w23}), pb, acc[b], 0, 0, 0);
+    }
+  }
+
+  lsum += xor_shfl(lsum, 16);
+  lsum += xor_shfl(lsum, 32);
+  if (!head_ok) return;
+
+  // acc[b][i] holds O[head c][d = DPL * (4 j + i) + b].
+  if (nparts == 1) {
+    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t w[DPL / 2];
+#pragma unroll
+      for (int b = 0; b < DPL; b += 2) w[b / 2] = pack_bf16x2(acc[b][i] * inv, acc[b + 1][i] * inv);
+      if constexpr (DPL == 8)
+        st16(out_row + DPL * i, u32x4{w[0], w[1], w[2], w[3]});
+      else
+        *reinterpret_cast<u32x2*>(out_row + DPL * i) = u32x2{w[0], w[1]};
+    }
+  } else {
+    const int64_t slot = ((int64_t)seq * a.num_heads + head) * a.max_parts + part;
+    float* dst = a.ws_acc + slot * D + DPL * 4 * j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int b = 0; b < DPL; b += 4)
+        *reinterpret_cast<f32x4*>(dst + DPL * i + b) =
+            f32x4{acc[b][i], acc[b + 1][i], acc[b + 2][i], acc[b + 3][i]};
+    }
+    if (j == 0) {
+      a.ws_ml[slot * 2] = m;
+      a.ws_ml[slot * 2 + 1] = lsum;
+    }
+  }
+}
+
+// Merge of the partition partials: one wave per (query head, sequence).
+template <int D>
+__global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
+  constexpr int PER_LANE = D / 64;
+  const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
+  const int64_t L = attended_len(a, seq);
+  const int nparts = L <= 0 ? 1 : (int)((L + a.part_tokens - 1) / a.part_tokens);
+  if (nparts <= 1) return;
+  const int64_t base = ((int64_t)seq * a.num_heads + head) * a.max_parts;
+  const float* ml = a.ws_ml + base * 2;
+
+  float mx = kNegInf;
+  for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, ml[2 * p]);
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, xor_shfl(mx, o));
+
+  float den = 0.f;
+  float acc[PER_LANE];
+#pragma unroll
+  for (int e = 0; e < PER_LANE; ++e) acc[e] = 0.f;
+  if (mx != kNegInf) {
+    for (int p = 0; p < nparts; ++p) {
+      const float mp = ml[2 * p];
+      const float w = mp == kNegInf ? 0.f : fast_exp2(mp - mx);
+      den += w * ml[2 * p + 1];
+      const float* src = a.ws_acc + (base + p) * D + lane * PER_LANE;
+#pragma unroll
+      for (int e = 0; e < PER_LANE; ++e) acc[e] += w * src[e];
+    }
+  }
+  const float inv = den > 0.f ? 1.f / den : 0.f;
+  u16* dst = a.out + ((int64_t)seq * a.num_heads + head) * D + lane * PER_LANE;
+  if constexpr (PER_LANE == 2)
+    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+  else
+    dst[0] = (u16)f32_to_bf16_bits(acc[0] * inv);
+}
+
+inline int decode_partition(int partition_tokens) {
+  int p = partition_tokens <= 0 ? kDecodeDefaultPartition : partition_tokens;
+  if (p % 16 != 0 || p > kDecodeMaxPartition) return -1;
+  return p;
+}
+
+inline int64_t decode_max_parts(int max_blocks, int part) {
+  return ((int64_t)max_blocks * 16 + part - 1) / part;
+}
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+}  // namespace ndl
+
+extern "C" size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
+                                                   int max_blocks_per_seq, int block_size,
+                                                   int partition_tokens) {
+  using namespace ndl;
+  const int part = decode_partition(partition_tokens);
+  if (part < 0 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0 ||
+      block_size != 16)
+    return 0;
+  const int64_t parts = decode_max_parts(max_blocks_per_seq, part);
+  if (parts <= 1) return 0;
+  const size_t slots = (size_t)num_seqs * num_heads * parts;
+  return align256(slots * 2 * sizeof(float)) + slots * head_dim * sizeof(float);
+}
+
+extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
+                                const void* kv_cache, int64_t num_blocks,
+                                const int32_t* block_table, int64_t bt_row_stride,
+                                int max_blocks_per_seq, const int32_t* context_lens, int num_seqs,
+                                int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                int dtype, float scale, int partition_tokens, void* workspace,
+                                size_t workspace_bytes, ndl_stream_t stream) {
+  using namespace ndl;
+  if (dtype != NDL_DTYPE_BF16) return NDL_ERR_UNSUPPORTED;
+  if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
+  if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
+    return NDL_ERR_INVALID_ARG;
+  const int group = num_heads / num_kv_heads;
+  if (group > 16) return NDL_ERR_UNSUPPORTED;
+  const int part = decode_partition(partition_tokens);
+  if (part < 0) return NDL_ERR_INVALID_ARG;
+  if (num_seqs < 0 || num_blocks <= 0 || max_blocks_per_seq <= 0 ||
+      bt_row_stride < max_blocks_per_seq || q_tok_stride < (int64_t)num_heads * head_dim)
+    return NDL_ERR_INVALID_ARG;
+  if (num_seqs == 0) return NDL_OK;
+  if (!out || !q || !kv_cache || !block_table || !context_lens) return NDL_ERR_INVALID_ARG;
+  if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)kv_cache) & 15u) return NDL_ERR_INVALID_ARG;
+  if (q_tok_stride & 7) return NDL_ERR_INVALID_ARG;
+  if (num_seqs > 65535 || num_kv_heads > 65535) return NDL_ERR_UNSUPPORTED;
+
+  const int64_t max_parts = decode_max_parts(max_blocks_per_seq, part);
+  const size_t need = ndl_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim,
+                                                       max_blocks_per_seq, block_size, part);
+  if (max_parts > 1 && (workspace == nullptr || workspace_bytes < need ||
+                        ((uintptr_t)workspace & 15u)))
+    return NDL_ERR_WORKSPACE;
+
+  DecodeArgs a;
+  a.out = (u16*)out;
+  a.q = (const u16*)q;
+  a.q_tok_stride = q_tok_stride;
+  a.kplane = (const u16*)kv_cache;
+  a.vplane = a.kplane + num_blocks * num_kv_heads * (int64_t)16 * head_dim;
+  a.num_blocks = num_blocks;
+  a.num_kv_heads = num_kv_heads;
+  a.block_table = block_table;
+  a.bt_row_stride = bt_row_stride;
+  a.max_blocks = max_blocks_per_seq;
+  a.context_lens = context_lens;
+  a.num_heads = num_heads;
+  a.group = group;
+  a.scale_log2 = scale * kLog2e;
+  a.part_tokens = part;
+  a.max_parts = (int)max_parts;
+  const size_t slots = (size_t)num_seqs * num_heads * max_parts;
+  a.ws_ml = (float*)workspace;
+  a.ws_acc = max_parts > 1 ? (float*)((char*)workspace + align256(slots * 2 * sizeof(float)))
+                           : nullptr;
+
+  hipStream_t s = (hipStream_t)stream;
+  const dim3 grid((unsigned)max_parts, (unsigned)num_kv_heads, (unsigned)num_seqs);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(paged_decode_kernel<128>, grid, dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL(paged_decode_kernel<64>, grid, dim3(64), 0, s, a);
+  int rc = check_launch();
+  if (rc != NDL_OK || max_parts <= 1) return rc;
+  const dim3 mgrid((unsigned)num_heads, (unsigned)num_seqs);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, s, a);
+  else
+    hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, s, a);
+  return check_launch();
+}

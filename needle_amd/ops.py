@@ -1,0 +1,216 @@
+"""torch-facing wrappers of the HIP paged-KV operations.
+
+Each function mirrors one seam of needle/layers/attention.py and forwards
+device pointers to the C ABI (include/needle_amd.h) on torch's current
+stream.  Nothing here computes on the host: the HIP library is required.
+
+Argument meaning follows the reference:
+  kv_cache      [2, num_blocks, num_kv_heads, block_size, head_dim]   (attention.py:9-10)
+  block_table   int32 [num_seqs, max_blocks_per_seq]                  (runner.py:220-235)
+  context_lens  int32 [num_seqs], tokens already cached               (runner.py:204-218)
+  cu_seqlens    int32 [num_seqs + 1], packed token offsets           (runner.py:217)
+"""
+from __future__ import annotations
+
+import os
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.NDL_DTYPE_BF16, torch.float16: _lib.NDL_DTYPE_F16}
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev: torch.device) -> int:
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _require(cond: bool, msg: str, exc=ValueError) -> None:
+    if not cond:
+        raise exc(msg)
+
+
+def _check_cache(kv_cache: torch.Tensor) -> None:
+    _require(kv_cache.dim() == 5 and kv_cache.shape[0] == 2,
+             f"kv_cache must be [2, num_blocks, num_kv_heads, block_size, head_dim], "
+             f"got {tuple(kv_cache.shape)}")
+    _require(kv_cache.is_cuda, "kv_cache must be a GPU tensor")
+    _require(kv_cache.is_contiguous(), "kv_cache must be contiguous")
+    _require(kv_cache.dtype in _DTYPES, f"unsupported kv_cache dtype {kv_cache.dtype}", TypeError)
+
+
+def _check_int32(name: str, t: torch.Tensor, dim: int, device) -> None:
+    _require(t.dtype == torch.int32, f"{name} must be int32, got {t.dtype}", TypeError)
+    _require(t.dim() == dim, f"{name} must have {dim} dims, got {t.dim()}")
+    _require(t.device == device, f"{name} must be on {device}, got {t.device}")
+    _require(t.stride(-1) == 1, f"{name} must be contiguous along its last dim")
+
+
+def _rows(name: str, x: torch.Tensor, n_heads: int, head_dim: int, device) -> int:
+    """Token stride of a [T, n_heads, head_dim] tensor with contiguous inner rows."""
+    _require(x.dim() == 3 and x.shape[1] == n_heads and x.shape[2] == head_dim,
+             f"{name} must be [T, {n_heads}, {head_dim}], got {tuple(x.shape)}")
+    _require(x.device == device, f"{name} must be on {device}")
+    _require(x.stride(2) == 1 and x.stride(1) == head_dim,
+             f"{name} rows must be contiguous (strides {x.stride()})")
+    return x.stride(0) if x.shape[0] > 1 else n_heads * head_dim
+
+
+def _validate_enabled() -> bool:
+    return os.environ.get("NEEDLE_AMD_VALIDATE", "") not in ("", "0")
+
+
+def _validate_slots(block_table, num_blocks, name="block_table") -> None:
+    """Opt-in host check (syncs) that mirrors the reference's index errors."""
+    if block_table.numel() == 0:
+        return
+    lo, hi = int(block_table.min()), int(block_table.max())
+    if lo < 0 or hi >= num_blocks:
+        raise IndexError(f"{name} holds block id outside [0, {num_blocks}): [{lo}, {hi}]")
+
+
+def kv_append(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor,
+              block_table: torch.Tensor, context_lens: torch.Tensor,
+              cu_seqlens: Optional[torch.Tensor] = None) -> None:
+    """Scatter k/v [T, Hkv, D] into kv_cache in place.
+
+    cu_seqlens=None is the decode form (attention.py:141-154: token i belongs
+    to sequence i); otherwise the varlen form of _write_kv (attention.py:204-246).
+    """
+    _check_cache(kv_cache)
+    dev = kv_cache.device
+    _, num_blocks, hkv, bs, d = kv_cache.shape
+    _require(k.dtype == kv_cache.dtype and v.dtype == kv_cache.dtype,
+             "k/v dtype must match kv_cache", TypeError)
+    ks = _rows("k", k, hkv, d, dev)
+    vs = _rows("v", v, hkv, d, dev)
+    _require(k.shape[0] == v.shape[0], "k and v token counts differ")
+    _check_int32("block_table", block_table, 2, dev)
+    _check_int32("context_lens", context_lens, 1, dev)
+    n_seqs = block_table.shape[0]
+    _require(context_lens.shape[0] == n_seqs, "context_lens/block_table batch mismatch")
+    n_tok = k.shape[0]
+    if cu_seqlens is None:
+        _require(n_tok == n_seqs, f"decode append needs one token per sequence "
+                 f"({n_tok} tokens, {n_seqs} sequences)")
+    else:
+        _check_int32("cu_seqlens", cu_seqlens, 1, dev)
+        _require(cu_seqlens.shape[0] == n_seqs + 1, "cu_seqlens must be [num_seqs + 1]")
+    if n_tok == 0:
+        return
+    _require(block_table.shape[1] > 0, "block_table has no columns")
+    if _validate_enabled():
+        _validate_slots(block_table, num_blocks)
+    lib = _lib.load()
+    rc = lib.ndl_kv_append(
+        kv_cache.data_ptr(), num_blocks, hkv, bs, d, _DTYPES[kv_cache.dtype],
+        k.data_ptr(), ks, v.data_ptr(), vs,
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        _ptr(cu_seqlens), context_lens.data_ptr(), n_seqs, n_tok, _stream(dev))
+    _lib.check(rc, "ndl_kv_append")
+
+
+def write_kv(k, v, kv_cache, block_table, cu_seqlens, context_lens) -> None:
+    """Same signature and effect as the reference _write_kv (attention.py:204-246)."""
+    kv_append(k, v, kv_cache, block_table, context_lens, cu_seqlens=cu_seqlens)
+
+
+def decode_workspace_bytes(num_seqs: int, num_heads: int, head_dim: int,
+                           max_blocks_per_seq: int, block_size: int = 16,
+                           partition_tokens: int = 0) -> int:
+    return int(_lib.load().ndl_paged_decode_workspace_bytes(
+        num_seqs, num_heads, head_dim, max_blocks_per_seq, block_size, partition_tokens))
+
+
+def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                 context_lens: torch.Tensor, scale: float, num_heads: int, num_kv_heads: int,
+                 head_dim: int, *, partition_tokens: int = 0,
+                 out: Optional[torch.Tensor] = None,
+                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Paged decode attention; same signature as _decode_pytorch (attention.py:291).
+
+    Sequence i attends min(context_lens[i] + 1, W * block_size) cached tokens.
+    Returns [num_seqs, num_heads, head_dim] in q's dtype.
+    """
+    _check_cache(kv_cache)
+    dev = kv_cache.device
+    _, num_blocks, hkv, bs, d = kv_cache.shape
+    _require(hkv == num_kv_heads and d == head_dim, "kv_cache shape disagrees with head counts")
+    _require(q.dtype == kv_cache.dtype, "q dtype must match kv_cache", TypeError)
+    qs = _rows("q", q, num_heads, head_dim, dev)
+    _check_int32("block_table", block_table, 2, dev)
+    _check_int32("context_lens", context_lens, 1, dev)
+    n_seqs = q.shape[0]
+    _require(block_table.shape[0] == n_seqs and context_lens.shape[0] == n_seqs,
+             "q / block_table / context_lens batch mismatch")
+    if out is None:
+        out = torch.empty((n_seqs, num_heads, head_dim), dtype=q.dtype, device=dev)
+    else:
+        _require(out.shape == (n_seqs, num_heads, head_dim) and out.is_contiguous()
+                 and out.dtype == q.dtype and out.device == dev, "bad out tensor")
+    if n_seqs == 0:
+        return out
+    _require(block_table.shape[1] > 0, "block_table has no columns")
+    if _validate_enabled():
+        _validate_slots(block_table, num_blocks)
+    lib = _lib.load()
+    w = block_table.shape[1]
+    need = int(lib.ndl_paged_decode_workspace_bytes(
+        n_seqs, num_heads, head_dim, w, bs, partition_tokens))
+    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
+    rc = lib.ndl_paged_decode(
+        out.data_ptr(), q.data_ptr(), qs, kv_cache.data_ptr(), num_blocks,
+        block_table.data_ptr(), block_table.stride(0), w,
+        context_lens.data_ptr(), n_seqs, num_heads, num_kv_heads, head_dim, bs,
+        _DTYPES[q.dtype], float(scale), partition_tokens, ws_ptr, need, _stream(dev))
+    _lib.check(rc, "ndl_paged_decode")
+    return out
+
+
+def varlen_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                   cu_seqlens: torch.Tensor, context_lens: torch.Tensor, max_seqlen: int,
+                   scale: float, num_heads: int, num_kv_heads: int, head_dim: int, *,
+                   max_context_len: int = 0,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Causal attention of packed prompts over the paged cache (after kv_append).
+
+    Equals the reference _prefill_pytorch (attention.py:120-134) when every
+    context_lens entry is 0; with a cached prefix the prefix is attended too.
+    Returns [num_tokens, num_heads, head_dim].
+    """
+    _check_cache(kv_cache)
+    dev = kv_cache.device
+    _, num_blocks, hkv, bs, d = kv_cache.shape
+    _require(hkv == num_kv_heads and d == head_dim, "kv_cache shape disagrees with head counts")
+    _require(q.dtype == kv_cache.dtype, "q dtype must match kv_cache", TypeError)
+    qs = _rows("q", q, num_heads, head_dim, dev)
+    _check_int32("block_table", block_table, 2, dev)
+    _check_int32("cu_seqlens", cu_seqlens, 1, dev)
+    _check_int32("context_lens", context_lens, 1, dev)
+    n_seqs = block_table.shape[0]
+    _require(cu_seqlens.shape[0] == n_seqs + 1 and context_lens.shape[0] == n_seqs,
+             "cu_seqlens / context_lens / block_table batch mismatch")
+    n_tok = q.shape[0]
+    if out is None:
+        out = torch.empty((n_tok, num_heads, head_dim), dtype=q.dtype, device=dev)
+    if n_tok == 0 or n_seqs == 0:
+        return out
+    _require(block_table.shape[1] > 0, "block_table has no columns")
+    if _validate_enabled():
+        _validate_slots(block_table, num_blocks)
+    lib = _lib.load()
+    rc = lib.ndl_varlen_prefill(
+        out.data_ptr(), q.data_ptr(), qs, kv_cache.data_ptr(), num_blocks,
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        cu_seqlens.data_ptr(), context_lens.data_ptr(), n_seqs, n_tok, int(max_seqlen),
+        int(max_context_len), num_heads, num_kv_heads, head_dim, bs, _DTYPES[q.dtype],
+        float(scale), _stream(dev))
+    _lib.check(rc, "ndl_varlen_prefill")
+    return out

@@ -1,0 +1,87 @@
+"""The C ABI library loads and exports what include/needle_amd.h declares.
+
+No kernel runs here (no GPU): only host-side entry points (version, status
+text, workspace sizing) and argument rejection paths that return before any
+HIP call.
+"""
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from needle_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "needle_amd.h"
+
+
+def declared_symbols():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ndl_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_and_binding_agree():
+    assert declared_symbols() == sorted(_lib.EXPORTED_SYMBOLS)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    for name in declared_symbols():
+        assert hasattr(raw, name), name
+
+
+def test_version_and_status_text(lib):
+    assert lib.ndl_abi_version() == _lib.NDL_ABI_VERSION
+    assert lib.ndl_strerror(0) == b"ok"
+    for code in (-1, -2, -3, -4):
+        assert lib.ndl_strerror(code) and lib.ndl_strerror(code) != b"unknown status"
+    assert lib.ndl_strerror(-99) == b"unknown status"
+
+
+def test_decode_workspace_sizing(lib):
+    # 2 sequences x 32 heads, W = 64 blocks = 1024 tokens, partitions of 256 -> 4 parts
+    n = lib.ndl_paged_decode_workspace_bytes(2, 32, 128, 64, 16, 256)
+    slots = 2 * 32 * 4
+    ml = (slots * 2 * 4 + 255) // 256 * 256
+    assert n == ml + slots * 128 * 4
+    # a single partition needs no scratch
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 128, 16, 16, 256) == 0
+    # unsupported block size / bad partition
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 128, 64, 32, 256) == 0
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 128, 64, 16, 100) == 0
+
+
+def test_rejections_before_any_launch(lib):
+    # unsupported dtype / head_dim / block size return without touching a device
+    rc = lib.ndl_kv_append(None, 1, 1, 16, 128, 7, None, 0, None, 0, None, 1, 1, None, None,
+                           1, 1, None)
+    assert rc == -2
+    rc = lib.ndl_paged_decode(None, None, 0, None, 1, None, 1, 1, None, 1, 4, 1, 96, 16, 0,
+                              1.0, 0, None, 0, None)
+    assert rc == -2
+    rc = lib.ndl_paged_decode(None, None, 0, None, 1, None, 1, 1, None, 1, 4, 1, 128, 32, 0,
+                              1.0, 0, None, 0, None)
+    assert rc == -2
+    rc = lib.ndl_paged_decode(None, None, 0, None, 1, None, 1, 1, None, 1, 40, 2, 128, 16, 0,
+                              1.0, 0, None, 0, None)
+    assert rc == -2  # group 20 > 16
+    # a non-multiple-of-16 partition
+    rc = lib.ndl_paged_decode(None, None, 512, None, 1, None, 1, 1, None, 1, 4, 1, 128, 16, 0,
+                              1.0, 24, None, 0, None)
+    assert rc == -1
+    # nothing to do: zero tokens / sequences
+    assert lib.ndl_kv_append(None, 1, 1, 16, 128, 0, None, 128, None, 128, None, 1, 1, None,
+                             None, 1, 0, None) == 0
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "_LIB", None)
+    monkeypatch.setenv("NEEDLE_AMD_LIB", str(tmp_path / "nope.so"))
+    with pytest.raises(_lib.NeedleAmdError):
+        _lib.load()

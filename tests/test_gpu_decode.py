@@ -1,0 +1,120 @@
+"""GPU parity of ndl_paged_decode against the oracle.
+
+Tolerance (bf16 in/out, fp32 accumulation): |gpu - ref| <= 2e-2 + 1e-2 |ref|,
+against both the reference restatement (bf16 op for op) and the fp64 closed
+form.  The append that precedes attention in _decode (attention.py:141-154)
+runs first on both sides.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import closed_form, paged_ref
+from needle_amd import ops, workloads as wl
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+ATOL, RTOL = 2e-2, 1e-2
+
+
+def assert_close(got, want, atol=ATOL, rtol=RTOL):
+    got = np.asarray(got, dtype=np.float64)
+    want = np.asarray(want, dtype=np.float64)
+    assert got.shape == want.shape
+    assert np.isfinite(got).all()
+    excess = np.abs(got - want) - (atol + rtol * np.abs(want))
+    worst = np.unravel_index(np.argmax(excess), excess.shape)
+    assert excess.max() <= 0, (
+        f"max |diff| {np.abs(got - want).max():.4g} at {worst}: "
+        f"got {got[worst]:.5g} want {want[worst]:.5g}")
+
+
+def run_gpu(case, partition_tokens=0):
+    g = case.to(DEV)
+    s = case.shape
+    ops.kv_append(g.k, g.v, g.kv_cache, g.block_table, g.context_lens)
+    out = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
+                           s.num_heads, s.num_kv_heads, s.head_dim,
+                           partition_tokens=partition_tokens)
+    torch.cuda.synchronize()
+    return out.float().cpu(), g
+
+
+def run_oracle(case):
+    s = case.shape
+    pool = case.kv_cache.clone()
+    out = paged_ref.decode(case.q, case.k, case.v, pool, case.block_table, case.context_lens,
+                           s.scale, s.num_heads, s.num_kv_heads, s.head_dim)
+    return out.float(), pool
+
+
+@pytest.mark.parametrize("cfg", [1, 2])
+def test_decode_configs_vs_oracle(cfg):
+    case = wl.config_case(cfg)
+    got, _ = run_gpu(case)
+    want, pool = run_oracle(case)
+    assert_close(got, want)
+    s = case.shape
+    ref64 = closed_form.decode_fp64(case.q, pool, case.block_table, case.context_lens, s.scale,
+                                    s.num_heads, s.num_kv_heads)
+    assert_close(got, ref64)
+
+
+@pytest.mark.parametrize("part", [16, 64, 256, 512, 1024])
+def test_partition_sizes_agree(part):
+    case = wl.decode_case(wl.LLAMA3_8B, [0, 15, 16, 255, 256, 257, 1023, 3000], seed=201)
+    got, _ = run_gpu(case, partition_tokens=part)
+    want, _ = run_oracle(case)
+    assert_close(got, want)
+
+
+@pytest.mark.parametrize("shape", [
+    wl.HeadShape(8, 8, 128), wl.HeadShape(16, 8, 128), wl.HeadShape(28, 4, 128),
+    wl.HeadShape(64, 8, 128), wl.HeadShape(16, 1, 128), wl.HeadShape(4, 4, 64),
+    wl.HeadShape(14, 2, 64), wl.HeadShape(12, 3, 64), wl.HeadShape(32, 2, 64)])
+def test_group_sizes_and_head_dims(shape):
+    case = wl.decode_case(shape, [0, 1, 17, 100, 600], seed=202)
+    got, _ = run_gpu(case)
+    want, _ = run_oracle(case)
+    assert_close(got, want)
+
+
+def test_single_token_context_is_exact_value_row():
+    case = wl.decode_case(wl.QWEN2_7B, [0, 0, 0, 0], seed=203)
+    got, _ = run_gpu(case)
+    g = case.shape.group
+    for h in range(case.shape.num_heads):
+        assert torch.equal(got[:, h], case.v[:, h // g].float())
+
+
+def test_row_width_cap():
+    # context 39 but two table columns: 32 tokens attended, like the reference slice
+    case = wl.decode_case(wl.LLAMA3_8B, [31, 20], seed=204)
+    case.context_lens = torch.tensor([39, 20], dtype=torch.int32)
+    case.ctx = [39, 20]
+    s = case.shape
+    g = case.to(DEV)
+    out = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
+                           s.num_heads, s.num_kv_heads, s.head_dim)
+    torch.cuda.synchronize()
+    want = paged_ref.decode_pytorch(case.q, case.kv_cache, case.block_table, case.context_lens,
+                                    s.scale, s.num_heads, s.num_kv_heads, s.head_dim)
+    assert_close(out.float().cpu(), want.float())
+
+
+def test_fragmented_long_context_sampled():
+    # configuration-5 style tables at reduced batch: allocator churn, contexts up to 32k
+    ctx = [1024, 32768, 8192, 4097, 20000, 1500]
+    case = wl.decode_case(wl.LLAMA3_8B, ctx, seed=205, table="allocator")
+    got, _ = run_gpu(case)
+    want, _ = run_oracle(case)
+    assert_close(got, want)
+
+
+def test_repeat_calls_are_deterministic():
+    case = wl.config_case(1)
+    a, g = run_gpu(case)
+    s = case.shape
+    b = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
+                         s.num_heads, s.num_kv_heads, s.head_dim).float().cpu()
+    assert torch.equal(a, b)
