@@ -1,0 +1,200 @@
+#!/usr/bin/env python3
+"""Benchmark of the paged-KV hot path on one MI355X.
+
+Workload (the Llama-3-8B decode step): 32 query / 8 kv heads, head_dim 128,
+block_size 16, 64 sequences with context U{512..4096} (seed 1002), one
+random non-contiguous block table shared by 32 layers, each layer with its own
+KV pool [2, NB, 8, 16, 128] bf16 (NB = 1.1 x the blocks in use; 32 pools
+~20 GB, far beyond the 256 MiB Infinity Cache, so every step streams from
+HBM).  One step = for each of the 32 layers: append one new K/V token per
+sequence, then paged decode attention over block_table.
+
+Printed (one JSON line):
+  value         algorithmic bytes of the whole step / step time   (GB/s)
+  roofline      paged decode alone: algorithmic bytes per launch / average
+                launch time, timed with events on the launch stream, vs the
+                8 TB/s HBM peak
+  cpu_baseline  the CPU restatement of the reference torch path, one layer
+                of the same workload, on this host's cores
+Algorithmic bytes: every attended K/V row once, q in, output out, the block
+table entries and context lengths read; for append, k/v rows read and
+written plus their slot indices.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+LAYERS = 32
+SEED = 1002
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--partition", type=int, default=0, help="decode partition tokens (0 = default)")
+    p.add_argument("--cpu-seconds", type=float, default=15.0,
+                   help="time budget of the CPU baseline sample")
+    p.add_argument("--no-cpu-baseline", action="store_true")
+    return p.parse_args()
+
+
+def build_workload(torch, wl, device):
+    shape = wl.LLAMA3_8B
+    ctx = wl.cfg2_ctx(SEED)
+    blocks = [(c + 1 + shape.block_size - 1) // shape.block_size for c in ctx]
+    num_blocks = int(math.ceil(sum(blocks) * 1.1))
+    tables = wl.tables_by_permutation(blocks, num_blocks, SEED)
+    bt = wl.pad_tables(tables, num_blocks).to(device)
+    ctx_t = torch.tensor(ctx, dtype=torch.int32, device=device)
+    gen = torch.Generator(device=device)
+    gen.manual_seed(SEED)
+    b, h, hkv, d = len(ctx), shape.num_heads, shape.num_kv_heads, shape.head_dim
+    pools, qs, ks, vs, outs = [], [], [], [], []
+    for _ in range(LAYERS):
+        pools.append(torch.randn((2, num_blocks, hkv, shape.block_size, d), generator=gen,
+                                 device=device, dtype=torch.bfloat16))
+        qs.append(torch.randn((b, h, d), generator=gen, device=device, dtype=torch.bfloat16))
+        ks.append(torch.randn((b, hkv, d), generator=gen, device=device, dtype=torch.bfloat16))
+        vs.append(torch.randn((b, hkv, d), generator=gen, device=device, dtype=torch.bfloat16))
+        outs.append(torch.empty((b, h, d), device=device, dtype=torch.bfloat16))
+    return shape, ctx, tables, num_blocks, bt, ctx_t, pools, qs, ks, vs, outs
+
+
+def time_region(torch, fn, reps):
+    """Average ms of fn() over reps, events on the current stream (where the kernels run)."""
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(reps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def cpu_baseline(torch, wl, shape, ctx, budget_s):
+    """The reference torch path on the CPU (append + _decode_pytorch), one layer, repeated."""
+    from oracle import paged_ref
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    case = wl.decode_case(shape, ctx, seed=SEED, device="cpu", garbage=False)
+    per_layer = wl.decode_bytes(shape, ctx, case.block_table.shape[1]) + \
+        wl.append_bytes(shape, len(ctx), len(ctx), varlen=False)
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        paged_ref.decode(case.q, case.k, case.v, case.kv_cache, case.block_table,
+                         case.context_lens, shape.scale, shape.num_heads, shape.num_kv_heads,
+                         shape.head_dim)
+        reps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or reps >= 1000:
+            break
+    return {"value": round(per_layer * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"one layer of the same workload (64 seqs, append + decode), "
+                      f"{reps} reps in {el:.1f} s, torch {torch.__version__} CPU, "
+                      f"{threads} threads"}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on exactly one GPU (asked for {args.gpus}); this build has no "
+              "multi-GPU path.", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from needle_amd import ops, workloads as wl
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    (shape, ctx, tables, num_blocks, bt, ctx_t, pools, qs, ks, vs,
+     outs) = build_workload(torch, wl, dev)
+    width = bt.shape[1]
+    ws_bytes = ops.decode_workspace_bytes(len(ctx), shape.num_heads, shape.head_dim, width,
+                                          shape.block_size, args.partition)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    h, hkv, d, sc = shape.num_heads, shape.num_kv_heads, shape.head_dim, shape.scale
+
+    def decode_layer(l):
+        ops.paged_decode(qs[l], pools[l], bt, ctx_t, sc, h, hkv, d,
+                         partition_tokens=args.partition, out=outs[l], workspace=ws)
+
+    def append_layer(l):
+        ops.kv_append(ks[l], vs[l], pools[l], bt, ctx_t)
+
+    def step():
+        for l in range(LAYERS):
+            append_layer(l)
+            decode_layer(l)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    ms_step = time_region(torch, step, args.steps)
+
+    # per-op timings over the same rotating pools
+    def decode_all():
+        for l in range(LAYERS):
+            decode_layer(l)
+
+    def append_all():
+        for l in range(LAYERS):
+            append_layer(l)
+
+    ms_dec = time_region(torch, decode_all, args.steps) / LAYERS
+    ms_app = time_region(torch, append_all, args.steps) / LAYERS
+
+    dec_b = wl.decode_bytes(shape, ctx, width)
+    app_b = wl.append_bytes(shape, len(ctx), len(ctx), varlen=False)
+    value = LAYERS * (dec_b + app_b) / (ms_step / 1e3) / 1e9
+    dec_gbs = dec_b / (ms_dec / 1e3) / 1e9
+    app_gbs = app_b / (ms_app / 1e3) / 1e9
+
+    result = {
+        "metric": "paged decode attn HBM GB/s (% of peak); KV-append GB/s; e2e output tok/s",
+        "value": round(value, 1),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "Llama-3-8B layer decode (32 layers): 32/8 heads, head_dim 128, "
+                        "block_size 16, batch 64, context U[512,4096], bf16, random "
+                        "non-contiguous block tables, append + paged decode per layer",
+            "layers": LAYERS, "batch": len(ctx), "context_tokens": sum(ctx),
+            "num_blocks_per_layer": num_blocks, "partition_tokens": args.partition or 1024,
+        },
+        "roofline": {
+            "bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "kernel": "paged decode (attention + partition merge), per layer launch",
+            "algorithmic_bytes_per_launch": dec_b, "avg_launch_us": round(ms_dec * 1e3, 2),
+        },
+        "kv_append": {"achieved_gbs": round(app_gbs, 1), "avg_launch_us": round(ms_app * 1e3, 2),
+                      "algorithmic_bytes_per_launch": app_b},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, wl, shape, ctx, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

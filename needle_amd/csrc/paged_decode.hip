@@ -20,11 +20,13 @@
 //   * Long contexts split into partitions of `part_tokens`; partials
 //     (m, l, unnormalised acc) go to the workspace and a second kernel
 //     merges them.  A sequence that fits one partition is written directly.
+#include <stdlib.h>
+
 #include "ndl_common.hpp"
 
 namespace ndl {
 
-constexpr int kDecodeDefaultPartition = 256;
+constexpr int kDecodeDefaultPartition = 1024;
 constexpr int kDecodeMaxPartition = 1024;  // 64 blocks: one table entry per lane
 
 template <int D> struct VRow;
@@ -33,7 +35,10 @@ template <> struct VRow<64> { using T = u32x2; };   // 4 bf16 per lane per token
 
 template <int D>
 __device__ __forceinline__ typename VRow<D>::T load_vrow(const u16* p) {
-  if constexpr (D == 128) return ld16(p); else return ld8(p);
+  if constexpr (D == 128)
+    return ldg16(p);
+  else
+    return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
 }
 
 // Element e (0..D/16-1) of the per-lane V row chunk, as raw bf16 bits in the low half.
@@ -70,13 +75,15 @@ __device__ __forceinline__ int64_t attended_len(const DecodeArgs& a, int seq) {
   return L < cap ? L : cap;
 }
 
-template <int D>
+template <int D, int NBUF>
 __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;   // k-steps of the QK^T MFMA
   constexpr int DPL = D / 16;  // head_dim elements per lane per V row
   using VT = typename VRow<D>::T;
 
-  const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+  // kv head is the fastest grid index: the 8 head slices of one block (adjacent in
+  // memory) are fetched by workgroups dispatched together.
+  const int kvh = blockIdx.x, part = blockIdx.y, seq = blockIdx.z;
   const int lane = threadIdx.x, j = lane >> 4, c = lane & 15;
   const int64_t L = attended_len(a, seq);
   const int nparts = L <= 0 ? 1 : (int)((L + a.part_tokens - 1) / a.part_tokens);
@@ -115,42 +122,65 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 
   const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
   const int64_t head_off = (int64_t)kvh * 16 * D;
-  const int k_off = c * D + 8 * j;        // token row c, head_dim chunk j (+32 s)
-  const int v_off = 4 * j * D + DPL * c;  // token rows 4j..4j+3, head_dim DPL*c..
+  // K is fetched in row layout (each load instruction reads RPI whole rows, 1 KiB
+  // contiguous), staged in LDS and read back in the MFMA A-operand layout.
+  constexpr int CPR = D / 8;      // 16-byte chunks per row
+  constexpr int RPI = 64 / CPR;   // rows per load instruction
+  const int k_row = lane / CPR, k_chunk = lane % CPR;
+  const int k_off = k_row * D + 8 * k_chunk;  // + RPI * D * s
+  const int v_off = 4 * j * D + DPL * c;      // token rows 4j..4j+3, head_dim DPL*c..
+  __shared__ __attribute__((aligned(16))) u16 ktile[16 * D];
+  // Chunk q of row r lives at r*D + 8*(q ^ swz(r)): conflict-free for both the
+  // row-layout writes and the A-operand reads.
+  auto swz = [](int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); };
 
   f32x4 acc[DPL];
 #pragma unroll
   for (int b = 0; b < DPL; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = kNegInf, lsum = 0.f;
 
-  for (int it = 0; it < ntiles; ++it) {
+  // One cache block (16 tokens) of K and V in registers.
+  struct Tile {
+    u32x4 k[KS];
+    VT v[4];
+    bool bad;
+  };
+
+  auto load_tile = [&](int it, Tile& t) {
     int64_t blk = __builtin_amdgcn_readlane(bt_lane, it);
-    const bool bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
-    if (bad) blk = 0;
+    t.bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
+    if (t.bad) blk = 0;
     const u16* kb = a.kplane + blk * blk_stride + head_off;
     const u16* vb = a.vplane + blk * blk_stride + head_off;
-
-    u32x4 kr[KS];
 #pragma unroll
-    for (int s = 0; s < KS; ++s) kr[s] = ld16(kb + k_off + 32 * s);
-    VT vr[4];
+    for (int s = 0; s < KS; ++s) t.k[s] = ldg16(kb + k_off + RPI * D * s);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) vr[i] = load_vrow<D>(vb + v_off + i * D);
+    for (int i = 0; i < 4; ++i) t.v[i] = load_vrow<D>(vb + v_off + i * D);
+  };
 
+  auto compute_tile = [&](int it, Tile& t) {
+    __builtin_amdgcn_wave_barrier();  // previous block's LDS reads are issued first
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const int r = RPI * s + k_row;
+      *reinterpret_cast<u32x4*>(ktile + r * D + 8 * (k_chunk ^ swz(r))) = t.k[s];
+    }
+    __builtin_amdgcn_wave_barrier();  // one wave: LDS executes its writes before its reads
     f32x4 st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int s = 0; s < KS; ++s)
-      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kr[s]), qb[s], st,
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 ka = *reinterpret_cast<const u32x4*>(ktile + c * D + 8 * ((j + 4 * s) ^ swz(c)));
+      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka), qb[s], st,
                                                    0, 0, 0);
-
+    }
     // st[i] is the score of token (tile0+it)*16 + 4j + i for head c.
     const int pos0 = (tile0 + it) * 16 + 4 * j;
-    const bool partial = bad || ((tile0 + it) * 16 + 16 > t1);  // wave-uniform
+    const bool partial = t.bad || ((tile0 + it) * 16 + 16 > t1);  // wave-uniform
     float sc[4];
     float mt = kNegInf;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const bool ok = !partial || (!bad && pos0 + i < t1);
+      const bool ok = !partial || (!t.bad && pos0 + i < t1);
       sc[i] = ok ? st[i] * a.scale_log2 : kNegInf;
       mt = fmaxf(mt, sc[i]);
     }
@@ -174,8 +204,8 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     if (partial) {  // masked rows may hold stale bits (NaN * 0 = NaN): clear them
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bool ok = !bad && pos0 + i < t1;
-        if (!ok) vr[i] = VT{};
+        const bool ok = !t.bad && pos0 + i < t1;
+        if (!ok) t.v[i] = VT{};
       }
     }
 
@@ -183,10 +213,24 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
         i16x4, u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])});
 #pragma unroll
     for (int b = 0; b < DPL; ++b) {
-      const uint32_t w01 = vrow_elem<D>(vr[0], b) | (vrow_elem<D>(vr[1], b) << 16);
-      const uint32_t w23 = vrow_elem<D>(vr[2], b) | (vrow_elem<D>(vr[3], b) << 16);
+      const uint32_t w01 = vrow_elem<D>(t.v[0], b) | (vrow_elem<D>(t.v[1], b) << 16);
+      const uint32_t w23 = vrow_elem<D>(t.v[2], b) | (vrow_elem<D>(t.v[3], b) << 16);
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
           __builtin_bit_cast(i16x4, u32x2{w01, w23}), pb, acc[b], 0, 0, 0);
+    }
+  };
+
+  // NBUF-deep ring: while block `it` computes, blocks it+1 .. it+NBUF-1 are in flight.
+  Tile buf[NBUF];
+#pragma unroll
+  for (int u = 0; u < NBUF - 1; ++u)
+    if (u < ntiles) load_tile(u, buf[u]);
+  for (int it = 0; it < ntiles; it += NBUF) {
+#pragma unroll
+    for (int u = 0; u < NBUF; ++u) {
+      const int nxt = it + u + NBUF - 1;
+      if (nxt < ntiles) load_tile(nxt, buf[(u + NBUF - 1) % NBUF]);
+      if (it + u < ntiles) compute_tile(it + u, buf[u]);
     }
   }
 
@@ -225,41 +269,73 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 }
 
 // Merge of the partition partials: one wave per (query head, sequence).
+// Pass 1 (lane-parallel over partitions): global max, weights w_p = 2^(m_p - M)
+// into LDS, denominator sum_p w_p l_p.  Pass 2: sum_p w_p acc_p with
+// independent, unrolled loads.
+constexpr int kMergeMaxParts = 2048;
+
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int PER_LANE = D / 64;
+  __shared__ float wsh[kMergeMaxParts];
   const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
   const int64_t L = attended_len(a, seq);
   const int nparts = L <= 0 ? 1 : (int)((L + a.part_tokens - 1) / a.part_tokens);
   if (nparts <= 1) return;
   const int64_t base = ((int64_t)seq * a.num_heads + head) * a.max_parts;
-  const float* ml = a.ws_ml + base * 2;
+  const float* __restrict__ ml = a.ws_ml + base * 2;
 
   float mx = kNegInf;
   for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, ml[2 * p]);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, xor_shfl(mx, o));
-
   float den = 0.f;
+  for (int p = lane; p < nparts; p += 64) {
+    const float mp = ml[2 * p];
+    const float w = (mp == kNegInf || mx == kNegInf) ? 0.f : fast_exp2(mp - mx);
+    wsh[p] = w;
+    den += w * ml[2 * p + 1];
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) den += xor_shfl(den, o);
+  __syncthreads();
+
   float acc[PER_LANE];
 #pragma unroll
   for (int e = 0; e < PER_LANE; ++e) acc[e] = 0.f;
-  if (mx != kNegInf) {
-    for (int p = 0; p < nparts; ++p) {
-      const float mp = ml[2 * p];
-      const float w = mp == kNegInf ? 0.f : fast_exp2(mp - mx);
-      den += w * ml[2 * p + 1];
-      const float* src = a.ws_acc + (base + p) * D + lane * PER_LANE;
+  const float* __restrict__ src = a.ws_acc + base * D + lane * PER_LANE;
+  int p = 0;
+  for (; p + 4 <= nparts; p += 4) {
+    float v[4][PER_LANE];
 #pragma unroll
-      for (int e = 0; e < PER_LANE; ++e) acc[e] += w * src[e];
-    }
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < PER_LANE; ++e) v[u][e] = src[(int64_t)(p + u) * D + e];
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < PER_LANE; ++e) acc[e] += wsh[p + u] * v[u][e];
   }
+  for (; p < nparts; ++p)
+#pragma unroll
+    for (int e = 0; e < PER_LANE; ++e) acc[e] += wsh[p] * src[(int64_t)p * D + e];
+
   const float inv = den > 0.f ? 1.f / den : 0.f;
   u16* dst = a.out + ((int64_t)seq * a.num_heads + head) * D + lane * PER_LANE;
   if constexpr (PER_LANE == 2)
     *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc[0] * inv, acc[1] * inv);
   else
     dst[0] = (u16)f32_to_bf16_bits(acc[0] * inv);
+}
+
+// Blocks in flight per wave (2..4).  NDL_DECODE_DEPTH overrides the default for tuning.
+inline int decode_pipeline_depth() {
+  static const int depth = [] {
+    const char* e = getenv("NDL_DECODE_DEPTH");
+    const int d = e ? atoi(e) : 2;
+    return (d >= 2 && d <= 4) ? d : 2;
+  }();
+  return depth;
 }
 
 inline int decode_partition(int partition_tokens) {
@@ -316,6 +392,7 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
   if (num_seqs > 65535 || num_kv_heads > 65535) return NDL_ERR_UNSUPPORTED;
 
   const int64_t max_parts = decode_max_parts(max_blocks_per_seq, part);
+  if (max_parts > kMergeMaxParts) return NDL_ERR_UNSUPPORTED;
   const size_t need = ndl_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim,
                                                        max_blocks_per_seq, block_size, part);
   if (max_parts > 1 && (workspace == nullptr || workspace_bytes < need ||
@@ -345,11 +422,23 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
                            : nullptr;
 
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)max_parts, (unsigned)num_kv_heads, (unsigned)num_seqs);
-  if (head_dim == 128)
-    hipLaunchKernelGGL(paged_decode_kernel<128>, grid, dim3(64), 0, s, a);
-  else
-    hipLaunchKernelGGL(paged_decode_kernel<64>, grid, dim3(64), 0, s, a);
+  const dim3 grid((unsigned)num_kv_heads, (unsigned)max_parts, (unsigned)num_seqs);
+  const int depth = decode_pipeline_depth();
+  if (head_dim == 128) {
+    if (depth == 2)
+      hipLaunchKernelGGL((paged_decode_kernel<128, 2>), grid, dim3(64), 0, s, a);
+    else if (depth == 4)
+      hipLaunchKernelGGL((paged_decode_kernel<128, 4>), grid, dim3(64), 0, s, a);
+    else
+      hipLaunchKernelGGL((paged_decode_kernel<128, 3>), grid, dim3(64), 0, s, a);
+  } else {
+    if (depth == 2)
+      hipLaunchKernelGGL((paged_decode_kernel<64, 2>), grid, dim3(64), 0, s, a);
+    else if (depth == 4)
+      hipLaunchKernelGGL((paged_decode_kernel<64, 4>), grid, dim3(64), 0, s, a);
+    else
+      hipLaunchKernelGGL((paged_decode_kernel<64, 3>), grid, dim3(64), 0, s, a);
+  }
   int rc = check_launch();
   if (rc != NDL_OK || max_parts <= 1) return rc;
   const dim3 mgrid((unsigned)num_heads, (unsigned)num_seqs);

@@ -89,7 +89,8 @@ def test_single_token_context_is_exact_value_row():
 
 def test_row_width_cap():
     # context 39 but two table columns: 32 tokens attended, like the reference slice
-    case = wl.decode_case(wl.LLAMA3_8B, [31, 20], seed=204)
+    # (every slot finite: no append runs here, so the attended slots are pre-filled)
+    case = wl.decode_case(wl.LLAMA3_8B, [31, 20], seed=204, garbage=False)
     case.context_lens = torch.tensor([39, 20], dtype=torch.int32)
     case.ctx = [39, 20]
     s = case.shape
