@@ -1,0 +1,96 @@
+"""Drop-in replacement for needle/layers/attention.py:Attention on MI355X.
+
+Same constructor, the same forward() signature and meaning
+(attention.py:36-96), the same parameter names (q_proj/k_proj/v_proj/o_proj),
+and the same KV pool layout [2, num_blocks, num_kv_heads, block_size,
+head_dim].  Projections and RoPE stay torch ops exactly as in the reference
+(attention.py:84-88, 277-288); the three paged-KV seams go to the HIP kernels:
+
+  _prefill  (attention.py:102-107): ndl_kv_append (varlen) + ndl_varlen_prefill
+  _decode   (attention.py:140-159): ndl_kv_append (one token per sequence)
+                                    + ndl_paged_decode
+
+No host synchronisation happens on either path: the decode split-K grid is
+sized from block_table's width, prefill from max_seqlen (both host-known).
+
+Tensor parallelism (tp_size > 1) is not built: one GPU holds every head.
+With context_lens > 0 in prefill the cached prefix is attended; the
+reference ignores it there (its TODO.md:29-32 records that as a bug), and its
+runner only ever passes 0 for prefill (runner.py:204-208).
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+import torch.nn as nn
+
+from .. import ops
+from ..model.config import ModelConfig
+
+
+def apply_rope(q, k, cos, sin):
+    """attention.py:277-283: x*cos + rotate_half(x)*sin on q [T,H,D] and k [T,Hkv,D]."""
+    cos = cos.unsqueeze(1)
+    sin = sin.unsqueeze(1)
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+def rotate_half(x):
+    """attention.py:286-288."""
+    half = x.shape[-1] // 2
+    return torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+
+
+class Attention(nn.Module):
+    """MHA / GQA attention over the paged KV cache (reference attention.py:33)."""
+
+    def __init__(self, config: ModelConfig, layer_idx: int, tp_size: int = 1, tp_rank: int = 0,
+                 qkv_bias: bool = False):
+        super().__init__()
+        if tp_size != 1:
+            raise NotImplementedError("needle_amd runs every head on one GPU (tp_size=1)")
+        self.layer_idx = layer_idx
+        self.num_heads = config.num_attention_heads
+        self.num_kv_heads = config.num_key_value_heads
+        self.head_dim = config.head_dim
+        self.scale = 1.0 / math.sqrt(self.head_dim)
+        hidden = config.hidden_size
+        self.q_proj = nn.Linear(hidden, self.num_heads * self.head_dim, bias=qkv_bias)
+        self.k_proj = nn.Linear(hidden, self.num_kv_heads * self.head_dim, bias=qkv_bias)
+        self.v_proj = nn.Linear(hidden, self.num_kv_heads * self.head_dim, bias=qkv_bias)
+        self.o_proj = nn.Linear(self.num_heads * self.head_dim, hidden, bias=False)
+        self._workspace = None
+
+    def forward(self, hidden_states: torch.Tensor, positions: torch.Tensor,
+                kv_cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens: torch.Tensor,
+                context_lens: torch.Tensor, max_seqlen: int, is_prefill: bool,
+                cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        total = hidden_states.shape[0]
+        q = self.q_proj(hidden_states).view(total, self.num_heads, self.head_dim)
+        k = self.k_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
+        v = self.v_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
+        q, k = apply_rope(q, k, cos, sin)
+        if is_prefill:
+            out = self._prefill(q, k, v, kv_cache, block_table, cu_seqlens, context_lens,
+                                max_seqlen)
+        else:
+            out = self._decode(q, k, v, kv_cache, block_table, context_lens)
+        return self.o_proj(out.view(total, self.num_heads * self.head_dim))
+
+    def _prefill(self, q, k, v, kv_cache, block_table, cu_seqlens, context_lens, max_seqlen):
+        ops.write_kv(k, v, kv_cache, block_table, cu_seqlens, context_lens)
+        return ops.varlen_prefill(q, kv_cache, block_table, cu_seqlens, context_lens,
+                                  int(max_seqlen), self.scale, self.num_heads,
+                                  self.num_kv_heads, self.head_dim)
+
+    def _decode(self, q, k, v, kv_cache, block_table, context_lens):
+        ops.kv_append(k, v, kv_cache, block_table, context_lens)
+        need = ops.decode_workspace_bytes(q.shape[0], self.num_heads, self.head_dim,
+                                          block_table.shape[1], kv_cache.shape[3])
+        ws = self._workspace
+        if need and (ws is None or ws.numel() < need or ws.device != q.device):
+            ws = self._workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        return ops.paged_decode(q, kv_cache, block_table, context_lens, self.scale,
+                                self.num_heads, self.num_kv_heads, self.head_dim,
+                                workspace=ws if need else None)

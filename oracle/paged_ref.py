@@ -111,3 +111,42 @@ def decode(q, k, v, kv_cache, block_table, context_lens, scale, num_heads, num_k
     decode_append(k, v, kv_cache, block_table, context_lens)
     return decode_pytorch(q, kv_cache, block_table, context_lens, scale,
                           num_heads, num_kv_heads, head_dim)
+
+
+def rotate_half(x):
+    """attention.py:286-288."""
+    half = x.shape[-1] // 2
+    return torch.cat([-x[..., half:], x[..., :half]], dim=-1)
+
+
+def apply_rope(q, k, cos, sin):
+    """attention.py:277-283."""
+    cos = cos.unsqueeze(1)
+    sin = sin.unsqueeze(1)
+    return q * cos + rotate_half(q) * sin, k * cos + rotate_half(k) * sin
+
+
+def attention_forward(weights, hidden_states, kv_cache, block_table, cu_seqlens, context_lens,
+                      is_prefill, cos, sin, num_heads, num_kv_heads, head_dim):
+    """attention.py:83-96 (Attention.forward, torch fallback path) with explicit weights.
+
+    weights: dict with q_proj/k_proj/v_proj/o_proj '.weight' (and optional
+    q/k/v '.bias') as the reference's Linear layers hold them (linear.py:49-50,
+    88-89); the projections are F.linear(x, w, b) (linear.py:54, 93-97).
+    """
+    t = hidden_states.shape[0]
+    q = F.linear(hidden_states, weights["q_proj.weight"], weights.get("q_proj.bias"))
+    k = F.linear(hidden_states, weights["k_proj.weight"], weights.get("k_proj.bias"))
+    v = F.linear(hidden_states, weights["v_proj.weight"], weights.get("v_proj.bias"))
+    q = q.view(t, num_heads, head_dim)
+    k = k.view(t, num_kv_heads, head_dim)
+    v = v.view(t, num_kv_heads, head_dim)
+    q, k = apply_rope(q, k, cos, sin)
+    scale = 1.0 / (head_dim ** 0.5)
+    if is_prefill:
+        out = prefill(q, k, v, kv_cache, block_table, cu_seqlens, context_lens, num_heads,
+                      num_kv_heads)
+    else:
+        out = decode(q, k, v, kv_cache, block_table, context_lens, scale, num_heads,
+                     num_kv_heads, head_dim)
+    return F.linear(out.reshape(t, num_heads * head_dim), weights["o_proj.weight"])
