@@ -30,6 +30,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 LAYERS = 32
 SEED = 1002
 
@@ -43,6 +44,8 @@ def parse_args():
     p.add_argument("--cpu-seconds", type=float, default=15.0,
                    help="time budget of the CPU baseline sample")
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--no-extras", action="store_true",
+                   help="skip the Qwen2-0.5B, Qwen2-7B prefill and long-context measurements")
     return p.parse_args()
 
 
@@ -80,6 +83,77 @@ def time_region(torch, fn, reps):
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
+
+
+def extra_measurements(torch, ops, wl, reps):
+    """The other four shapes, one launch sequence each (event timing on the launch stream)."""
+    dev = torch.device("cuda:0")
+    res = {}
+
+    # Qwen2-0.5B layer decode, 8 sequences: ~1 MB working set, cache-resident.
+    c1 = wl.config_case(1, device=dev, garbage=False)
+    s1 = c1.shape
+
+    def dec1():
+        ops.kv_append(c1.k, c1.v, c1.kv_cache, c1.block_table, c1.context_lens)
+        ops.paged_decode(c1.q, c1.kv_cache, c1.block_table, c1.context_lens, s1.scale,
+                         s1.num_heads, s1.num_kv_heads, s1.head_dim)
+    dec1()
+    ms1 = time_region(torch, dec1, reps * 10)
+    b1 = wl.decode_bytes(s1, c1.ctx, c1.block_table.shape[1]) + \
+        wl.append_bytes(s1, c1.num_seqs, c1.num_seqs, varlen=False)
+    res["qwen2_0.5b_decode"] = {"us_per_layer": round(ms1 * 1e3, 2),
+                                "effective_gbs": round(b1 / ms1 / 1e6, 1),
+                                "note": "append + decode of 8 sequences; ~1 MB working set "
+                                        "stays in L2/MALL (cache-resident, not an HBM figure)"}
+    del c1
+
+    # Qwen2-7B varlen prefill: append all prompt tokens, then causal attention.
+    c3 = wl.config_case(3, device=dev, garbage=False)
+    s3 = c3.shape
+
+    def app3():
+        ops.write_kv(c3.k, c3.v, c3.kv_cache, c3.block_table, c3.cu_seqlens, c3.context_lens)
+
+    def att3():
+        ops.varlen_prefill(c3.q, c3.kv_cache, c3.block_table, c3.cu_seqlens, c3.context_lens,
+                           c3.max_seqlen, s3.scale, s3.num_heads, s3.num_kv_heads, s3.head_dim)
+    app3()
+    att3()
+    ms_a = time_region(torch, app3, reps)
+    ms_p = time_region(torch, att3, reps)
+    t3 = sum(c3.new_lens)
+    ab = wl.append_bytes(s3, t3, c3.num_seqs, varlen=True)
+    fl = wl.prefill_flops(s3, c3.new_lens)
+    res["qwen2_7b_prefill"] = {
+        "tokens": t3, "append_us": round(ms_a * 1e3, 2),
+        "append_gbs": round(ab / ms_a / 1e6, 1),
+        "append_frac_of_hbm_peak": round(ab / ms_a / 1e6 / HBM_PEAK_GBS, 4),
+        "attention_us": round(ms_p * 1e3, 2),
+        "attention_tflops": round(fl / ms_p / 1e9, 1),
+        "attention_frac_of_mfma_peak": round(fl / ms_p / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "algorithmic_flops": fl}
+    del c3
+
+    # Llama-3-8B long-context fragmented decode, 256 sequences, allocator-churned tables.
+    c5 = wl.config_case(5, device=dev, garbage=False)
+    s5 = c5.shape
+
+    def dec5():
+        ops.kv_append(c5.k, c5.v, c5.kv_cache, c5.block_table, c5.context_lens)
+        ops.paged_decode(c5.q, c5.kv_cache, c5.block_table, c5.context_lens, s5.scale,
+                         s5.num_heads, s5.num_kv_heads, s5.head_dim)
+    dec5()
+    ms5 = time_region(torch, dec5, max(3, reps // 4))
+    b5 = wl.decode_bytes(s5, c5.ctx, c5.block_table.shape[1]) + \
+        wl.append_bytes(s5, c5.num_seqs, c5.num_seqs, varlen=False)
+    res["llama3_8b_long_context_decode"] = {
+        "ms": round(ms5, 4), "gbs": round(b5 / ms5 / 1e6, 1),
+        "frac_of_hbm_peak": round(b5 / ms5 / 1e6 / HBM_PEAK_GBS, 4),
+        "context_tokens": sum(c5.ctx), "lognormal_sigma": wl.CFG5_SIGMA}
+    del c5
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(torch, wl, shape, ctx, budget_s):
@@ -191,6 +265,10 @@ def main():
         "kv_append": {"achieved_gbs": round(app_gbs, 1), "avg_launch_us": round(ms_app * 1e3, 2),
                       "algorithmic_bytes_per_launch": app_b},
     }
+    if not args.no_extras:
+        del pools
+        torch.cuda.empty_cache()
+        result["other_shapes"] = extra_measurements(torch, ops, wl, max(args.steps // 5, 5))
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, wl, shape, ctx, args.cpu_seconds)
     print(json.dumps(result), flush=True)

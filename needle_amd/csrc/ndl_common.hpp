@@ -23,16 +23,22 @@ constexpr float kNegInf = -__builtin_huge_valf();
 __device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
-// fp32 -> bf16 with round-to-nearest-even; NaN stays NaN.
-__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return (u >> 16) | 0x40u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+
+// fp32 pair -> packed bf16 pair, round-to-nearest-even (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{lo, hi}, bf16x2));
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return f32_to_bf16_bits(lo) | (f32_to_bf16_bits(hi) << 16);
+// fp32 -> bf16 bits (low half), round-to-nearest-even.
+__device__ __forceinline__ uint32_t f32_to_bf16_bits(float f) {
+  return pack_bf16x2(f, 0.f) & 0xffffu;
+}
+
+// Pack the low (sel_hi = false) or high halves of two words: {lo.half, hi.half}.
+__device__ __forceinline__ uint32_t pack_halves(uint32_t lo, uint32_t hi, bool high_half) {
+  return __builtin_amdgcn_perm(hi, lo, high_half ? 0x07060302u : 0x05040100u);
 }
 
 // exp2 on the hardware transcendental unit (v_exp_f32).

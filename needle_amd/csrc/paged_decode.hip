@@ -41,13 +41,6 @@ __device__ __forceinline__ typename VRow<D>::T load_vrow(const u16* p) {
     return __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
 }
 
-// Element e (0..D/16-1) of the per-lane V row chunk, as raw bf16 bits in the low half.
-template <int D>
-__device__ __forceinline__ uint32_t vrow_elem(const typename VRow<D>::T& r, int e) {
-  const uint32_t w = r[e >> 1];
-  return (e & 1) ? (w >> 16) : (w & 0xffffu);
-}
-
 struct DecodeArgs {
   u16* out;
   const u16* q;
@@ -198,8 +191,10 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     }
     lsum = lsum * alpha + ps;
     m = m_new;
+    if (__ballot(alpha != 1.f)) {  // rescale only when some head's max moved
 #pragma unroll
-    for (int b = 0; b < DPL; ++b) acc[b] *= alpha;
+      for (int b = 0; b < DPL; ++b) acc[b] *= alpha;
+    }
 
     if (partial) {  // masked rows may hold stale bits (NaN * 0 = NaN): clear them
 #pragma unroll
@@ -213,8 +208,8 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
         i16x4, u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])});
 #pragma unroll
     for (int b = 0; b < DPL; ++b) {
-      const uint32_t w01 = vrow_elem<D>(t.v[0], b) | (vrow_elem<D>(t.v[1], b) << 16);
-      const uint32_t w23 = vrow_elem<D>(t.v[2], b) | (vrow_elem<D>(t.v[3], b) << 16);
+      const uint32_t w01 = pack_halves(t.v[0][b >> 1], t.v[1][b >> 1], b & 1);
+      const uint32_t w23 = pack_halves(t.v[2][b >> 1], t.v[3][b >> 1], b & 1);
       acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
           __builtin_bit_cast(i16x4, u32x2{w01, w23}), pb, acc[b], 0, 0, 0);
     }
