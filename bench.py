@@ -46,12 +46,15 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true",
                    help="skip the Qwen2-0.5B, Qwen2-7B prefill and long-context measurements")
+    p.add_argument("--profile", action="store_true",
+                   help="counter-collection driver: --steps steps of the workload, then three "
+                        "1 GiB device copies (the calibration kernel), no timing output")
     return p.parse_args()
 
 
 def build_workload(torch, wl, device):
     shape = wl.LLAMA3_8B
-    ctx = wl.cfg2_ctx(SEED)
+    ctx = wl.llama8b_decode_ctx(SEED)
     blocks = [(c + 1 + shape.block_size - 1) // shape.block_size for c in ctx]
     num_blocks = int(math.ceil(sum(blocks) * 1.1))
     tables = wl.tables_by_permutation(blocks, num_blocks, SEED)
@@ -69,6 +72,22 @@ def build_workload(torch, wl, device):
         vs.append(torch.randn((b, hkv, d), generator=gen, device=device, dtype=torch.bfloat16))
         outs.append(torch.empty((b, h, d), device=device, dtype=torch.bfloat16))
     return shape, ctx, tables, num_blocks, bt, ctx_t, pools, qs, ks, vs, outs
+
+
+TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                               "paged_decode_llama3_8b_hbm_traffic.md")
+
+
+def measured_traffic():
+    """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE summary (or None)."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def time_region(torch, fn, reps):
@@ -91,7 +110,7 @@ def extra_measurements(torch, ops, wl, reps):
     res = {}
 
     # Qwen2-0.5B layer decode, 8 sequences: ~1 MB working set, cache-resident.
-    c1 = wl.config_case(1, device=dev, garbage=False)
+    c1 = wl.config_case("qwen2-0.5b-decode", device=dev, garbage=False)
     s1 = c1.shape
 
     def dec1():
@@ -109,7 +128,7 @@ def extra_measurements(torch, ops, wl, reps):
     del c1
 
     # Qwen2-7B varlen prefill: append all prompt tokens, then causal attention.
-    c3 = wl.config_case(3, device=dev, garbage=False)
+    c3 = wl.config_case("qwen2-7b-prefill", device=dev, garbage=False)
     s3 = c3.shape
 
     def app3():
@@ -136,7 +155,7 @@ def extra_measurements(torch, ops, wl, reps):
     del c3
 
     # Llama-3-8B long-context fragmented decode, 256 sequences, allocator-churned tables.
-    c5 = wl.config_case(5, device=dev, garbage=False)
+    c5 = wl.config_case("llama3-8b-long-decode", device=dev, garbage=False)
     s5 = c5.shape
 
     def dec5():
@@ -150,7 +169,7 @@ def extra_measurements(torch, ops, wl, reps):
     res["llama3_8b_long_context_decode"] = {
         "ms": round(ms5, 4), "gbs": round(b5 / ms5 / 1e6, 1),
         "frac_of_hbm_peak": round(b5 / ms5 / 1e6 / HBM_PEAK_GBS, 4),
-        "context_tokens": sum(c5.ctx), "lognormal_sigma": wl.CFG5_SIGMA}
+        "context_tokens": sum(c5.ctx), "lognormal_sigma": wl.LONG_CONTEXT_SIGMA}
     del c5
     torch.cuda.empty_cache()
     return res
@@ -213,6 +232,20 @@ def main():
             append_layer(l)
             decode_layer(l)
 
+    if args.profile:
+        for _ in range(args.steps):
+            step()
+        src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_steps": args.steps, "layers": LAYERS,
+                          "decode_algorithmic_bytes_per_launch":
+                              wl.decode_bytes(shape, ctx, width),
+                          "calibration_copy_bytes_read": src.numel() * 2}), flush=True)
+        return
+
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -258,7 +291,10 @@ def main():
         },
         "roofline": {
             "bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+            "traffic": measured_traffic(),
+            "traffic_source": "profiles/paged_decode_llama3_8b_hbm_traffic.md (rocprofv3 "
+                              "FETCH_SIZE x2 + WRITE_SIZE x1, scaled by a 1 GiB copy)",
             "kernel": "paged decode (attention + partition merge), per layer launch",
             "algorithmic_bytes_per_launch": dec_b, "avg_launch_us": round(ms_dec * 1e3, 2),
         },

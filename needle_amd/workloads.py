@@ -1,15 +1,16 @@
-"""Seeded synthetic inputs for the paged-KV path, at the five benchmark shapes.
+"""Seeded synthetic inputs for the paged-KV path at the benchmark shapes.
 
-Shapes and distributions:
-  1  Qwen2-0.5B layer decode: 14/2 heads, head_dim 64, 8 sequences,
-     context U{32..512}, 512-block pool, table = random permutation
-  2  Llama-3-8B layer decode: 32/8 heads, head_dim 128, 64 sequences,
-     context U{512..4096}, random non-contiguous tables
-  3  Qwen2-7B varlen prefill: 28/4 heads, head_dim 128, 16 prompts U{128..2048}
-  5  Llama-3-8B long-context decode: 256 sequences, context
-     lognormal(median 8192, sigma 1.0) clipped to [1024, 32768], tables from
-     10,000 seeded alloc/free cycles of BlockAllocator
-(4 is the end-to-end engine run, built elsewhere.)
+Named cases (CASES):
+  qwen2-0.5b-decode     Qwen2-0.5B layer decode: 14/2 heads, head_dim 64, 8
+                        sequences, context U{32..512}, 512-block pool, table =
+                        random permutation
+  llama3-8b-decode      Llama-3-8B layer decode: 32/8 heads, head_dim 128, 64
+                        sequences, context U{512..4096}, random non-contiguous tables
+  qwen2-7b-prefill      Qwen2-7B varlen prefill: 28/4 heads, head_dim 128, 16
+                        prompts U{128..2048} packed by cu_seqlens
+  llama3-8b-long-decode Llama-3-8B long-context decode: 256 sequences, context
+                        lognormal(median 8192, sigma 1.0) clipped to [1024, 32768],
+                        tables from 10,000 seeded alloc/free cycles of BlockAllocator
 
 Values are bf16 ~N(0, 1).  Cache slots no sequence owns hold random bit
 patterns (NaN and Inf included) so that a stray read or write shows.  The
@@ -235,39 +236,44 @@ def prefill_case(shape: HeadShape, seq_lens: List[int], *, seed: int, device="cp
 # the benchmark configurations
 # ----------------------------------------------------------------------------
 
-def cfg1_ctx(seed: int = 1001) -> List[int]:
+def qwen05b_decode_ctx(seed: int = 1001) -> List[int]:
     return np.random.default_rng(seed).integers(32, 512, size=8, endpoint=True).tolist()
 
 
-def cfg2_ctx(seed: int = 1002, batch: int = 64) -> List[int]:
+def llama8b_decode_ctx(seed: int = 1002, batch: int = 64) -> List[int]:
     return np.random.default_rng(seed).integers(512, 4096, size=batch, endpoint=True).tolist()
 
 
-def cfg3_lens(seed: int = 1003, prompts: int = 16) -> List[int]:
+def qwen7b_prefill_lens(seed: int = 1003, prompts: int = 16) -> List[int]:
     return np.random.default_rng(seed).integers(128, 2048, size=prompts, endpoint=True).tolist()
 
 
-CFG5_SIGMA = 1.0
+LONG_CONTEXT_SIGMA = 1.0
 
 
-def cfg5_ctx(seed: int = 1005, batch: int = 256, sigma: float = CFG5_SIGMA) -> List[int]:
+def llama8b_long_ctx(seed: int = 1005, batch: int = 256, sigma: float = LONG_CONTEXT_SIGMA) -> List[int]:
     r = np.random.default_rng(seed).lognormal(math.log(8192.0), sigma, size=batch)
     return np.clip(np.round(r), 1024, 32768).astype(np.int64).tolist()
 
 
-def config_case(cfg: int, device="cpu", garbage: bool = True) -> PagedCase:
-    """Full-size inputs of configuration 1, 2, 3 or 5."""
-    if cfg == 1:
-        return decode_case(QWEN2_05B, cfg1_ctx(), seed=1001, device=device, num_blocks=512,
+CASES = ("qwen2-0.5b-decode", "llama3-8b-decode", "qwen2-7b-prefill", "llama3-8b-long-decode")
+
+
+def config_case(name: str, device="cpu", garbage: bool = True) -> PagedCase:
+    """Full-size inputs of one named case (see CASES)."""
+    if name == "qwen2-0.5b-decode":
+        return decode_case(QWEN2_05B, qwen05b_decode_ctx(), seed=1001, device=device,
+                           num_blocks=512, garbage=garbage)
+    if name == "llama3-8b-decode":
+        return decode_case(LLAMA3_8B, llama8b_decode_ctx(), seed=1002, device=device,
                            garbage=garbage)
-    if cfg == 2:
-        return decode_case(LLAMA3_8B, cfg2_ctx(), seed=1002, device=device, garbage=garbage)
-    if cfg == 3:
-        return prefill_case(QWEN2_7B, cfg3_lens(), seed=1003, device=device, garbage=garbage)
-    if cfg == 5:
-        return decode_case(LLAMA3_8B, cfg5_ctx(), seed=1005, device=device, table="allocator",
-                           garbage=garbage)
-    raise ValueError(f"no paged-attention case for configuration {cfg}")
+    if name == "qwen2-7b-prefill":
+        return prefill_case(QWEN2_7B, qwen7b_prefill_lens(), seed=1003, device=device,
+                            garbage=garbage)
+    if name == "llama3-8b-long-decode":
+        return decode_case(LLAMA3_8B, llama8b_long_ctx(), seed=1005, device=device,
+                           table="allocator", garbage=garbage)
+    raise ValueError(f"unknown case {name!r}; known: {', '.join(CASES)}")
 
 
 # ----------------------------------------------------------------------------

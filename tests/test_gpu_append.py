@@ -35,8 +35,8 @@ def _varlen_parity(case):
     assert torch.equal(_bits(g.kv_cache.cpu()), _bits(want))
 
 
-@pytest.mark.parametrize("cfg", [1, 2])
-def test_decode_append_configs(cfg):
+@pytest.mark.parametrize("cfg", ["qwen2-0.5b-decode", "llama3-8b-decode"])
+def test_decode_append_named_cases(cfg):
     _decode_parity(wl.config_case(cfg))
 
 
@@ -46,8 +46,8 @@ def test_decode_append_block_edges():
     _decode_parity(wl.decode_case(wl.QWEN2_05B, [0, 15, 16, 17, 31, 32, 1000], seed=102))
 
 
-def test_varlen_append_config3():
-    _varlen_parity(wl.config_case(3))
+def test_varlen_append_qwen2_7b_prefill():
+    _varlen_parity(wl.config_case("qwen2-7b-prefill"))
 
 
 def test_varlen_append_prefix_and_empty_seqs():

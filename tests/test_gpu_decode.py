@@ -48,8 +48,8 @@ def run_oracle(case):
     return out.float(), pool
 
 
-@pytest.mark.parametrize("cfg", [1, 2])
-def test_decode_configs_vs_oracle(cfg):
+@pytest.mark.parametrize("cfg", ["qwen2-0.5b-decode", "llama3-8b-decode"])
+def test_decode_named_cases_vs_oracle(cfg):
     case = wl.config_case(cfg)
     got, _ = run_gpu(case)
     want, pool = run_oracle(case)
@@ -104,7 +104,7 @@ def test_row_width_cap():
 
 
 def test_fragmented_long_context_sampled():
-    # configuration-5 style tables at reduced batch: allocator churn, contexts up to 32k
+    # long-context style tables at reduced batch: allocator churn, contexts up to 32k
     ctx = [1024, 32768, 8192, 4097, 20000, 1500]
     case = wl.decode_case(wl.LLAMA3_8B, ctx, seed=205, table="allocator")
     got, _ = run_gpu(case)
@@ -113,7 +113,7 @@ def test_fragmented_long_context_sampled():
 
 
 def test_repeat_calls_are_deterministic():
-    case = wl.config_case(1)
+    case = wl.config_case("qwen2-0.5b-decode")
     a, g = run_gpu(case)
     s = case.shape
     b = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,

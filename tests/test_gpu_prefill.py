@@ -49,16 +49,16 @@ def oracle(case):
     return out.float(), pool
 
 
-def test_config3_vs_oracle():
-    case = wl.config_case(3)
+def test_qwen2_7b_prefill_vs_oracle():
+    case = wl.config_case("qwen2-7b-prefill")
     got, pool = run_gpu(case)
     want, want_pool = oracle(case)
     assert torch.equal(pool.view(torch.int16), want_pool.view(torch.int16))
     assert_close(got, want)
 
 
-def test_config3_sampled_rows_vs_fp64():
-    case = wl.config_case(3)
+def test_qwen2_7b_prefill_sampled_rows_vs_fp64():
+    case = wl.config_case("qwen2-7b-prefill")
     got, pool = run_gpu(case)
     s = case.shape
     # fp64 closed form on a sample of sequences: the two shortest and two longest prompts
