@@ -287,7 +287,7 @@ def main():
                         "block_size 16, batch 64, context U[512,4096], bf16, random "
                         "non-contiguous block tables, append + paged decode per layer",
             "layers": LAYERS, "batch": len(ctx), "context_tokens": sum(ctx),
-            "num_blocks_per_layer": num_blocks, "partition_tokens": args.partition or 1024,
+            "num_blocks_per_layer": num_blocks, "partition_tokens": args.partition or "auto (1024 here)",
         },
         "roofline": {
             "bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,

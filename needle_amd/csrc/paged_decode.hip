@@ -26,7 +26,7 @@
 
 namespace ndl {
 
-constexpr int kDecodeDefaultPartition = 1024;
+constexpr int kDecodeMinAutoPartition = 64;
 constexpr int kDecodeMaxPartition = 1024;  // 64 blocks: one table entry per lane
 
 template <int D> struct VRow;
@@ -265,9 +265,11 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
 
 // Merge of the partition partials: one wave per (query head, sequence).
 // Pass 1 (lane-parallel over partitions): global max, weights w_p = 2^(m_p - M)
-// into LDS, denominator sum_p w_p l_p.  Pass 2: sum_p w_p acc_p with
-// independent, unrolled loads.
+// into LDS, denominator sum_p w_p l_p.  Pass 2: sum_p w_p acc_p; the first
+// kMergePrefetch partials were loaded together with the (m, l) pairs, the rest
+// with independent, unrolled loads.
 constexpr int kMergeMaxParts = 2048;
+constexpr int kMergePrefetch = 8;
 
 template <int D>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
@@ -279,6 +281,14 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   if (nparts <= 1) return;
   const int64_t base = ((int64_t)seq * a.num_heads + head) * a.max_parts;
   const float* __restrict__ ml = a.ws_ml + base * 2;
+  const float* __restrict__ src = a.ws_acc + base * D + lane * PER_LANE;
+
+  // The first partials do not depend on the weights: load them with the (m, l) pairs.
+  float pre[kMergePrefetch][PER_LANE];
+#pragma unroll
+  for (int u = 0; u < kMergePrefetch; ++u)
+#pragma unroll
+    for (int e = 0; e < PER_LANE; ++e) pre[u][e] = u < nparts ? src[(int64_t)u * D + e] : 0.f;
 
   float mx = kNegInf;
   for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, ml[2 * p]);
@@ -298,8 +308,12 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   float acc[PER_LANE];
 #pragma unroll
   for (int e = 0; e < PER_LANE; ++e) acc[e] = 0.f;
-  const float* __restrict__ src = a.ws_acc + base * D + lane * PER_LANE;
-  int p = 0;
+#pragma unroll
+  for (int u = 0; u < kMergePrefetch; ++u)
+    if (u < nparts)
+#pragma unroll
+      for (int e = 0; e < PER_LANE; ++e) acc[e] += wsh[u] * pre[u][e];
+  int p = kMergePrefetch;
   for (; p + 4 <= nparts; p += 4) {
     float v[4][PER_LANE];
 #pragma unroll
@@ -333,9 +347,18 @@ inline int decode_pipeline_depth() {
   return depth;
 }
 
-inline int decode_partition(int partition_tokens) {
-  int p = partition_tokens <= 0 ? kDecodeDefaultPartition : partition_tokens;
-  if (p % 16 != 0 || p > kDecodeMaxPartition) return -1;
+// Partition size.  The default aims at ~16k waves' worth of (sequence, head, partition)
+// slots: W*16*B*H / 16384 tokens, rounded up to a power of two in [64, 1024].  Small
+// batches get short partitions (enough waves to cover the GPU); large ones get long
+// partitions (few partials to merge).
+inline int decode_partition(int partition_tokens, int num_seqs, int num_heads, int max_blocks) {
+  if (partition_tokens > 0) {
+    if (partition_tokens % 16 != 0 || partition_tokens > kDecodeMaxPartition) return -1;
+    return partition_tokens;
+  }
+  const double work = (double)max_blocks * 16.0 * num_seqs * num_heads / 16384.0;
+  int p = kDecodeMinAutoPartition;
+  while (p < kDecodeMaxPartition && p < work) p <<= 1;
   return p;
 }
 
@@ -351,10 +374,11 @@ extern "C" size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, 
                                                    int max_blocks_per_seq, int block_size,
                                                    int partition_tokens) {
   using namespace ndl;
-  const int part = decode_partition(partition_tokens);
-  if (part < 0 || num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0 ||
+  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0 ||
       block_size != 16)
     return 0;
+  const int part = decode_partition(partition_tokens, num_seqs, num_heads, max_blocks_per_seq);
+  if (part < 0) return 0;
   const int64_t parts = decode_max_parts(max_blocks_per_seq, part);
   if (parts <= 1) return 0;
   const size_t slots = (size_t)num_seqs * num_heads * parts;
@@ -375,8 +399,6 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
     return NDL_ERR_INVALID_ARG;
   const int group = num_heads / num_kv_heads;
   if (group > 16) return NDL_ERR_UNSUPPORTED;
-  const int part = decode_partition(partition_tokens);
-  if (part < 0) return NDL_ERR_INVALID_ARG;
   if (num_seqs < 0 || num_blocks <= 0 || max_blocks_per_seq <= 0 ||
       bt_row_stride < max_blocks_per_seq || q_tok_stride < (int64_t)num_heads * head_dim)
     return NDL_ERR_INVALID_ARG;
@@ -385,6 +407,8 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
   if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)kv_cache) & 15u) return NDL_ERR_INVALID_ARG;
   if (q_tok_stride & 7) return NDL_ERR_INVALID_ARG;
   if (num_seqs > 65535 || num_kv_heads > 65535) return NDL_ERR_UNSUPPORTED;
+  const int part = decode_partition(partition_tokens, num_seqs, num_heads, max_blocks_per_seq);
+  if (part < 0) return NDL_ERR_INVALID_ARG;
 
   const int64_t max_parts = decode_max_parts(max_blocks_per_seq, part);
   if (max_parts > kMergeMaxParts) return NDL_ERR_UNSUPPORTED;
