@@ -1,0 +1,106 @@
+"""Qwen2 / Llama decoder models around the paged-KV Attention.
+
+Structure and parameter names follow needle/model/qwen2.py:22-109 and
+needle/model/llama.py:18-140 of the reference:
+  decoder layer = RMSNorm -> Attention (+residual) -> RMSNorm -> SwiGLU MLP (+residual)
+  (qwen2.py:52-65); SwiGLU = down(silu(gate(x)) * up(x)) (llama.py:36-37);
+  Qwen2 adds biases to q/k/v (qwen2.py:22-39); the causal-LM head applies
+  lm_head to the last token of each prefill sequence, or to every decode token
+  (qwen2.py:100-109).
+Tensor parallelism is not built (one GPU).
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from ..layers.attention import Attention
+from ..layers.norm import RMSNorm
+from ..layers.rope import RotaryEmbedding
+from .config import ModelConfig
+
+
+class MLP(nn.Module):
+    def __init__(self, config: ModelConfig):
+        super().__init__()
+        self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
+        self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
+        self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class DecoderLayer(nn.Module):
+    def __init__(self, config: ModelConfig, layer_idx: int, qkv_bias: bool):
+        super().__init__()
+        self.self_attn = Attention(config, layer_idx, qkv_bias=qkv_bias)
+        self.mlp = MLP(config)
+        self.input_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+
+    def forward(self, hidden_states, positions, kv_cache, block_table, cu_seqlens, context_lens,
+                max_seqlen, is_prefill, cos, sin):
+        residual = hidden_states
+        h = self.input_layernorm(hidden_states)
+        h = self.self_attn(h, positions, kv_cache, block_table, cu_seqlens, context_lens,
+                           max_seqlen, is_prefill, cos, sin)
+        h = residual + h
+        residual = h
+        h = self.post_attention_layernorm(h)
+        return residual + self.mlp(h)
+
+
+class DecoderModel(nn.Module):
+    def __init__(self, config: ModelConfig, qkv_bias: bool):
+        super().__init__()
+        self.embed_tokens = nn.Embedding(config.vocab_size, config.hidden_size)
+        self.layers = nn.ModuleList(
+            [DecoderLayer(config, i, qkv_bias) for i in range(config.num_hidden_layers)])
+        self.norm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
+        self.rotary_emb = RotaryEmbedding(config.head_dim, config.max_position_embeddings,
+                                          config.rope_theta)
+
+    def forward(self, input_ids, positions, kv_caches, block_table, cu_seqlens, context_lens,
+                max_seqlen, is_prefill):
+        cos, sin = self.rotary_emb.get_cos_sin(positions)
+        h = self.embed_tokens(input_ids)
+        for i, layer in enumerate(self.layers):
+            h = layer(h, positions, kv_caches[i], block_table, cu_seqlens, context_lens,
+                      max_seqlen, is_prefill, cos, sin)
+        return self.norm(h)
+
+
+class CausalLM(nn.Module):
+    """Qwen2ForCausalLM (qkv_bias=True) / LlamaForCausalLM (qkv_bias=False)."""
+
+    def __init__(self, config: ModelConfig, qkv_bias: bool):
+        super().__init__()
+        self.config = config
+        self.model = DecoderModel(config, qkv_bias)
+        self.lm_head = nn.Linear(config.hidden_size, config.vocab_size, bias=False)
+
+    def forward(self, input_ids, positions, kv_caches, block_table, cu_seqlens, context_lens,
+                max_seqlen, is_prefill):
+        h = self.model(input_ids, positions, kv_caches, block_table, cu_seqlens, context_lens,
+                       max_seqlen, is_prefill)
+        last = h[cu_seqlens[1:].long() - 1] if is_prefill else h
+        return self.lm_head(last)
+
+
+def build_model(config: ModelConfig) -> CausalLM:
+    """needle/model/__init__.py:8: qwen2 -> Qwen2ForCausalLM, otherwise Llama."""
+    return CausalLM(config, qkv_bias=config.model_type == "qwen2")
+
+
+@torch.no_grad()
+def random_init_(model: nn.Module, seed: int, std: float = 0.02) -> nn.Module:
+    """Synthetic weights: every Linear/Embedding weight and bias ~N(0, std), norms = 1."""
+    g = torch.Generator(device="cpu").manual_seed(seed)
+    for name, p in model.named_parameters():
+        if name.endswith("layernorm.weight") or name.endswith("norm.weight"):
+            p.fill_(1.0)
+        else:
+            p.copy_(torch.randn(p.shape, generator=g) * std)
+    return model
