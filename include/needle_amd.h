@@ -6,6 +6,8 @@
  *
  *   ndl_kv_append       scatter new K/V rows into the block pool
  *                       (decode append attention.py:141-154, _write_kv :204-246)
+ *   ndl_rope_kv_append  rotary embedding of q/k fused with that append
+ *                       (_apply_rope :88, :277-288)
  *   ndl_paged_decode    one-query-per-sequence attention over block_table
  *                       (_decode_pytorch :291-310, dispatched from _decode :156-159;
  *                        also covers the FlashInfer wrapper :161-197)
@@ -89,6 +91,32 @@ int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int bloc
                   const int32_t* block_table, int64_t bt_row_stride, int max_blocks_per_seq,
                   const int32_t* cu_seqlens, const int32_t* context_lens,
                   int num_seqs, int64_t num_tokens, ndl_stream_t stream);
+
+/*
+ * Rotary embedding of q and k fused with the K/V append.
+ *
+ * Replaces: needle/layers/attention.py:88 (_apply_rope, :277-288) followed by
+ *           the append of attention.py:141-154 (decode) or :204-246 (_write_kv).
+ *
+ * For every token t and every element d < head_dim, with half = head_dim / 2,
+ *   rot(x)[d] = -x[d + half] (d < half), x[d - half] (d >= half)
+ *   y[d]      = bf16( bf16(x[d] * cos[t][d]) + bf16(rot(x)[d] * sin[t][d]) )
+ * which is the reference's op-by-op bf16 rounding (bit-exact).  q rotated is
+ * written to q_out [num_tokens][num_heads][head_dim] (contiguous); k rotated and
+ * v unchanged go to the cache slot that ndl_kv_append would pick for token t
+ * (same slot rule, same handling of out-of-range block ids).  cos/sin:
+ * [num_tokens][head_dim] with token stride cs_tok_stride.  head_dim must be a
+ * multiple of 16; bf16 only.
+ */
+int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stride,
+                       const void* k, int64_t k_tok_stride,
+                       const void* v, int64_t v_tok_stride,
+                       const void* cos, const void* sin, int64_t cs_tok_stride,
+                       void* kv_cache, int64_t num_blocks, int num_heads, int num_kv_heads,
+                       int block_size, int head_dim, int dtype,
+                       const int32_t* block_table, int64_t bt_row_stride, int max_blocks_per_seq,
+                       const int32_t* cu_seqlens, const int32_t* context_lens,
+                       int num_seqs, int64_t num_tokens, ndl_stream_t stream);
 
 /*
  * Bytes of scratch ndl_paged_decode needs for this shape.  partition_tokens

@@ -24,6 +24,7 @@ EXPORTED_SYMBOLS = (
     "ndl_abi_version",
     "ndl_strerror",
     "ndl_kv_append",
+    "ndl_rope_kv_append",
     "ndl_paged_decode_workspace_bytes",
     "ndl_paged_decode",
     "ndl_varlen_prefill",
@@ -41,6 +42,14 @@ _SIGNATURES = {
     "ndl_kv_append": (_c_i32, [
         _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32,   # cache, NB, Hkv, bs, D, dtype
         _c_p, _c_i64, _c_p, _c_i64,                     # k, k stride, v, v stride
+        _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
+        _c_p, _c_p, _c_i32, _c_i64, _c_p,               # cu, ctx, B, T, stream
+    ]),
+    "ndl_rope_kv_append": (_c_i32, [
+        _c_p, _c_p, _c_i64,                             # q_out, q, q stride
+        _c_p, _c_i64, _c_p, _c_i64,                     # k, k stride, v, v stride
+        _c_p, _c_p, _c_i64,                             # cos, sin, cos/sin stride
+        _c_p, _c_i64, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,  # cache, NB, H, Hkv, bs, D, dtype
         _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
         _c_p, _c_p, _c_i32, _c_i64, _c_p,               # cu, ctx, B, T, stream
     ]),

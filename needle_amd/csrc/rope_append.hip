@@ -1,0 +1,215 @@
+// Fused rotary embedding + KV append.
+//
+// Reference: needle/layers/attention.py:88 with _apply_rope / _rotate_half
+// (:277-288), followed by the decode append (:141-154) or _write_kv (:204-246).
+// The reference runs ~8 elementwise kernels for RoPE on q and k, then the
+// scatter; here one launch rotates q (written to q_out), rotates k and copies v
+// straight into their cache slots.
+//
+// Rounding is the reference's, op for op, in bf16:
+//   out[d] = bf16( bf16(x[d] * cos[d]) + bf16(rot(x)[d] * sin[d]) )
+// with rot(x)[d] = -x[d + D/2] (d < D/2) or x[d - D/2] (d >= D/2); every
+// product and the sum are formed in fp32 from bf16 operands and rounded to
+// nearest-even, exactly as torch does for bf16 tensors.  The result is
+// bit-identical to the reference's.
+#include "ndl_common.hpp"
+
+namespace ndl {
+
+__device__ __forceinline__ int seq_of_token_rope(const int32_t* __restrict__ cu, int n,
+                                                 int64_t t) {
+  int lo = 0, hi = n - 1;
+  while (lo < hi) {
+    int mid = (lo + hi + 1) >> 1;
+    if ((int64_t)cu[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+__device__ __forceinline__ float round_bf16(float x) {
+  return __uint_as_float(f32_to_bf16_bits(x) << 16);
+}
+
+// 8 bf16 of x[d..d+8) and x[d+D/2..d+D/2+8) -> rotated halves.
+__device__ __forceinline__ void rope8(const u32x4& lo, const u32x4& hi, const u32x4& clo,
+                                      const u32x4& chi, const u32x4& slo, const u32x4& shi,
+                                      u32x4& out_lo, u32x4& out_hi) {
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    float a[2], b[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const float xl = h ? bf16_hi(lo[w]) : bf16_lo(lo[w]);
+      const float xh = h ? bf16_hi(hi[w]) : bf16_lo(hi[w]);
+      const float cl = h ? bf16_hi(clo[w]) : bf16_lo(clo[w]);
+      const float ch = h ? bf16_hi(chi[w]) : bf16_lo(chi[w]);
+      const float sl = h ? bf16_hi(slo[w]) : bf16_lo(slo[w]);
+      const float sh = h ? bf16_hi(shi[w]) : bf16_lo(shi[w]);
+      // first half: x*cos + (-x_hi)*sin ; second half: x_hi*cos + x*sin
+      a[h] = round_bf16(xl * cl) + round_bf16(-xh * sl);
+      b[h] = round_bf16(xh * ch) + round_bf16(xl * sh);
+    }
+    out_lo[w] = pack_bf16x2(a[0], a[1]);
+    out_hi[w] = pack_bf16x2(b[0], b[1]);
+  }
+}
+
+struct RopeArgs {
+  u16* q_out;
+  const u16* q;
+  int64_t q_tok_stride;
+  const u16* k;
+  int64_t k_tok_stride;
+  const u16* v;
+  int64_t v_tok_stride;
+  const u16* cos;
+  const u16* sin;
+  int64_t cs_tok_stride;
+  u16* cache;
+  int64_t plane_elems;
+  int64_t num_blocks;
+  int num_heads;
+  int num_kv_heads;
+  int block_size;
+  int head_dim;
+  const int32_t* block_table;
+  int64_t bt_row_stride;
+  int max_blocks;
+  const int32_t* cu_seqlens;
+  const int32_t* context_lens;
+  int num_seqs;
+  int64_t num_tokens;
+};
+
+// Element offset of (token t, kv head h) in the K plane, by the append's slot rule
+// (attention.py:143-146, :224-237); false when the slot is out of range.
+__device__ __forceinline__ bool kv_slot(const RopeArgs& a, int64_t t, int h, int64_t& off) {
+  int i;
+  int64_t p;
+  if (a.cu_seqlens == nullptr) {
+    i = (int)t;
+    p = a.context_lens[i];
+  } else {
+    if (t >= (int64_t)a.cu_seqlens[a.num_seqs]) return false;
+    i = seq_of_token_rope(a.cu_seqlens, a.num_seqs, t);
+    p = (int64_t)a.context_lens[i] + (t - a.cu_seqlens[i]);
+  }
+  if (p < 0) return false;
+  int64_t col = p / a.block_size;
+  if (col > a.max_blocks - 1) col = a.max_blocks - 1;
+  const int64_t blk = a.block_table[(int64_t)i * a.bt_row_stride + col];
+  if (blk < 0 || blk >= a.num_blocks) return false;
+  off = ((blk * a.num_kv_heads + h) * a.block_size + p % a.block_size) * (int64_t)a.head_dim;
+  return true;
+}
+
+// One thread per (token, row, 8-element chunk of the first half).  Rows 0..H-1 are q
+// heads, H..H+Hkv-1 k heads, H+Hkv..H+2Hkv-1 v heads (copied, not rotated).
+__global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
+  const int half = a.head_dim >> 1;
+  const int cph = half >> 3;  // chunks per half row
+  const int rows = a.num_heads + 2 * a.num_kv_heads;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= a.num_tokens * rows * cph) return;
+  const int c = (int)(idx % cph);
+  const int64_t rt = idx / cph;
+  const int row = (int)(rt % rows);
+  const int64_t t = rt / rows;
+  const int d0 = 8 * c;
+
+  if (row >= a.num_heads + a.num_kv_heads) {  // v: both halves copied into the V plane
+    const int h = row - a.num_heads - a.num_kv_heads;
+    int64_t off;
+    if (!kv_slot(a, t, h, off)) return;
+    const u16* src = a.v + t * a.v_tok_stride + (int64_t)h * a.head_dim;
+    u16* dst = a.cache + a.plane_elems + off;
+    st16(dst + d0, ld16(src + d0));
+    st16(dst + d0 + half, ld16(src + d0 + half));
+    return;
+  }
+
+  const u16* cs = a.cos + t * a.cs_tok_stride;
+  const u16* sn = a.sin + t * a.cs_tok_stride;
+  const u32x4 clo = ld16(cs + d0), chi = ld16(cs + d0 + half);
+  const u32x4 slo = ld16(sn + d0), shi = ld16(sn + d0 + half);
+  u32x4 olo, ohi;
+  u16* dst;
+  const u16* src;
+  if (row < a.num_heads) {  // q: rotated into q_out [T][H][D]
+    src = a.q + t * a.q_tok_stride + (int64_t)row * a.head_dim;
+    dst = a.q_out + (t * a.num_heads + row) * (int64_t)a.head_dim;
+  } else {                  // k: rotated into its K-plane slot
+    const int h = row - a.num_heads;
+    int64_t off;
+    if (!kv_slot(a, t, h, off)) return;
+    src = a.k + t * a.k_tok_stride + (int64_t)h * a.head_dim;
+    dst = a.cache + off;
+  }
+  rope8(ld16(src + d0), ld16(src + d0 + half), clo, chi, slo, shi, olo, ohi);
+  st16(dst + d0, olo);
+  st16(dst + d0 + half, ohi);
+}
+
+}  // namespace ndl
+
+extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stride,
+                                  const void* k, int64_t k_tok_stride, const void* v,
+                                  int64_t v_tok_stride, const void* cos, const void* sin,
+                                  int64_t cs_tok_stride, void* kv_cache, int64_t num_blocks,
+                                  int num_heads, int num_kv_heads, int block_size, int head_dim,
+                                  int dtype, const int32_t* block_table, int64_t bt_row_stride,
+                                  int max_blocks_per_seq, const int32_t* cu_seqlens,
+                                  const int32_t* context_lens, int num_seqs, int64_t num_tokens,
+                                  ndl_stream_t stream) {
+  using namespace ndl;
+  if (dtype != NDL_DTYPE_BF16) return NDL_ERR_UNSUPPORTED;
+  if (head_dim <= 0 || head_dim % 16 != 0 || block_size <= 0) return NDL_ERR_UNSUPPORTED;
+  if (num_tokens < 0 || num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
+      max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq)
+    return NDL_ERR_INVALID_ARG;
+  if (num_tokens == 0) return NDL_OK;
+  if (!q_out || !q || !k || !v || !cos || !sin || !kv_cache || !block_table || !context_lens ||
+      num_seqs == 0)
+    return NDL_ERR_INVALID_ARG;
+  if (cu_seqlens == nullptr && num_tokens != num_seqs) return NDL_ERR_INVALID_ARG;
+  if (q_tok_stride < (int64_t)num_heads * head_dim ||
+      k_tok_stride < (int64_t)num_kv_heads * head_dim ||
+      v_tok_stride < (int64_t)num_kv_heads * head_dim || cs_tok_stride < head_dim)
+    return NDL_ERR_INVALID_ARG;
+  if (((uintptr_t)q_out | (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)cos |
+       (uintptr_t)sin | (uintptr_t)kv_cache) & 15u)
+    return NDL_ERR_INVALID_ARG;
+  if ((q_tok_stride | k_tok_stride | v_tok_stride | cs_tok_stride) & 7) return NDL_ERR_INVALID_ARG;
+
+  RopeArgs a;
+  a.q_out = (u16*)q_out;
+  a.q = (const u16*)q;
+  a.q_tok_stride = q_tok_stride;
+  a.k = (const u16*)k;
+  a.k_tok_stride = k_tok_stride;
+  a.v = (const u16*)v;
+  a.v_tok_stride = v_tok_stride;
+  a.cos = (const u16*)cos;
+  a.sin = (const u16*)sin;
+  a.cs_tok_stride = cs_tok_stride;
+  a.cache = (u16*)kv_cache;
+  a.plane_elems = num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
+  a.num_blocks = num_blocks;
+  a.num_heads = num_heads;
+  a.num_kv_heads = num_kv_heads;
+  a.block_size = block_size;
+  a.head_dim = head_dim;
+  a.block_table = block_table;
+  a.bt_row_stride = bt_row_stride;
+  a.max_blocks = max_blocks_per_seq;
+  a.cu_seqlens = cu_seqlens;
+  a.context_lens = context_lens;
+  a.num_seqs = num_seqs;
+  a.num_tokens = num_tokens;
+  const int64_t total = num_tokens * (num_heads + 2 * num_kv_heads) * (head_dim / 16);
+  const int64_t blocks = (total + 255) / 256;
+  if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
+  hipLaunchKernelGGL(rope_kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0,
+                     (hipStream_t)stream, a);
+  return check_launch();
+}

@@ -3,8 +3,16 @@
 Same constructor, the same forward() signature and meaning
 (attention.py:36-96), the same parameter names (q_proj/k_proj/v_proj/o_proj),
 and the same KV pool layout [2, num_blocks, num_kv_heads, block_size,
-head_dim].  Projections and RoPE stay torch ops exactly as in the reference
-(attention.py:84-88, 277-288); the three paged-KV seams go to the HIP kernels:
+head_dim].  Projections stay torch GEMMs (attention.py:84-86).  RoPE
+(attention.py:88, 277-288) and the K/V append run as one HIP launch
+(ndl_rope_kv_append, bit-exact with the reference's bf16 rounding), then:
+
+  prefill (attention.py:102-107): ndl_varlen_prefill
+  decode  (attention.py:140-159): ndl_paged_decode
+
+The reference's two seams stay available with their own signatures, taking
+q and k already rotated, for callers that apply RoPE themselves
+(fuse_rope = False selects them inside forward):
 
   _prefill  (attention.py:102-107): ndl_kv_append (varlen) + ndl_varlen_prefill
   _decode   (attention.py:140-159): ndl_kv_append (one token per sequence)
@@ -61,6 +69,7 @@ class Attention(nn.Module):
         self.v_proj = nn.Linear(hidden, self.num_kv_heads * self.head_dim, bias=qkv_bias)
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, hidden, bias=False)
         self._workspace = None
+        self.fuse_rope = True
 
     def forward(self, hidden_states: torch.Tensor, positions: torch.Tensor,
                 kv_cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens: torch.Tensor,
@@ -70,22 +79,38 @@ class Attention(nn.Module):
         q = self.q_proj(hidden_states).view(total, self.num_heads, self.head_dim)
         k = self.k_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
         v = self.v_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
-        q, k = apply_rope(q, k, cos, sin)
-        if is_prefill:
-            out = self._prefill(q, k, v, kv_cache, block_table, cu_seqlens, context_lens,
-                                max_seqlen)
+        if self.fuse_rope:
+            q = ops.rope_kv_append(q, k, v, cos, sin, kv_cache, block_table, context_lens,
+                                   cu_seqlens if is_prefill else None)
+            if is_prefill:
+                out = self._prefill_attend(q, kv_cache, block_table, cu_seqlens, context_lens,
+                                           max_seqlen)
+            else:
+                out = self._decode_attend(q, kv_cache, block_table, context_lens)
         else:
-            out = self._decode(q, k, v, kv_cache, block_table, context_lens)
+            q, k = apply_rope(q, k, cos, sin)
+            if is_prefill:
+                out = self._prefill(q, k, v, kv_cache, block_table, cu_seqlens, context_lens,
+                                    max_seqlen)
+            else:
+                out = self._decode(q, k, v, kv_cache, block_table, context_lens)
         return self.o_proj(out.view(total, self.num_heads * self.head_dim))
 
     def _prefill(self, q, k, v, kv_cache, block_table, cu_seqlens, context_lens, max_seqlen):
         ops.write_kv(k, v, kv_cache, block_table, cu_seqlens, context_lens)
+        return self._prefill_attend(q, kv_cache, block_table, cu_seqlens, context_lens,
+                                    max_seqlen)
+
+    def _prefill_attend(self, q, kv_cache, block_table, cu_seqlens, context_lens, max_seqlen):
         return ops.varlen_prefill(q, kv_cache, block_table, cu_seqlens, context_lens,
                                   int(max_seqlen), self.scale, self.num_heads,
                                   self.num_kv_heads, self.head_dim)
 
     def _decode(self, q, k, v, kv_cache, block_table, context_lens):
         ops.kv_append(k, v, kv_cache, block_table, context_lens)
+        return self._decode_attend(q, kv_cache, block_table, context_lens)
+
+    def _decode_attend(self, q, kv_cache, block_table, context_lens):
         need = ops.decode_workspace_bytes(q.shape[0], self.num_heads, self.head_dim,
                                           block_table.shape[1], kv_cache.shape[3])
         ws = self._workspace

@@ -115,6 +115,68 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor,
     _lib.check(rc, "ndl_kv_append")
 
 
+def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
+                   sin: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
+                   context_lens: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Rotate q/k by (cos, sin) and append rotated k and v to kv_cache; returns rotated q.
+
+    Same result as _apply_rope (attention.py:88, :277-288) followed by the append
+    of attention.py:141-154 (cu_seqlens=None) or _write_kv (:204-246), bit for bit.
+    q [T, H, D], k/v [T, Hkv, D], cos/sin [T, D] in the cache dtype (bf16).
+    """
+    _check_cache(kv_cache)
+    dev = kv_cache.device
+    _, num_blocks, hkv, bs, d = kv_cache.shape
+    _require(kv_cache.dtype == torch.bfloat16, "rope_kv_append supports bfloat16 only", TypeError)
+    for name, x in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
+        _require(x.dtype == kv_cache.dtype, f"{name} dtype must match kv_cache", TypeError)
+    _require(q.dim() == 3, f"q must be [T, H, {d}], got {tuple(q.shape)}")
+    h = q.shape[1]
+    qs = _rows("q", q, h, d, dev)
+    ks = _rows("k", k, hkv, d, dev)
+    vs = _rows("v", v, hkv, d, dev)
+    n_tok = q.shape[0]
+    _require(k.shape[0] == n_tok and v.shape[0] == n_tok, "q/k/v token counts differ")
+    _require(h % hkv == 0, f"num_heads {h} not a multiple of num_kv_heads {hkv}")
+    _require(d % 16 == 0, f"head_dim {d} must be a multiple of 16")
+    for name, x in (("cos", cos), ("sin", sin)):
+        _require(x.dim() == 2 and x.shape[0] == n_tok and x.shape[1] == d,
+                 f"{name} must be [{n_tok}, {d}], got {tuple(x.shape)}")
+        _require(x.device == dev and x.stride(1) == 1, f"{name} rows must be contiguous on {dev}")
+    _require(cos.stride(0) == sin.stride(0) or n_tok <= 1, "cos and sin token strides differ")
+    cs = cos.stride(0) if n_tok > 1 else d
+    _check_int32("block_table", block_table, 2, dev)
+    _check_int32("context_lens", context_lens, 1, dev)
+    n_seqs = block_table.shape[0]
+    _require(context_lens.shape[0] == n_seqs, "context_lens/block_table batch mismatch")
+    if cu_seqlens is None:
+        _require(n_tok == n_seqs, f"decode append needs one token per sequence "
+                 f"({n_tok} tokens, {n_seqs} sequences)")
+    else:
+        _check_int32("cu_seqlens", cu_seqlens, 1, dev)
+        _require(cu_seqlens.shape[0] == n_seqs + 1, "cu_seqlens must be [num_seqs + 1]")
+    if out is None:
+        out = torch.empty((n_tok, h, d), dtype=q.dtype, device=dev)
+    else:
+        _require(out.shape == (n_tok, h, d) and out.is_contiguous() and out.dtype == q.dtype
+                 and out.device == dev, "out must be a contiguous [T, H, D] tensor like q")
+    if n_tok == 0:
+        return out
+    _require(block_table.shape[1] > 0, "block_table has no columns")
+    if _validate_enabled():
+        _validate_slots(block_table, num_blocks)
+    lib = _lib.load()
+    rc = lib.ndl_rope_kv_append(
+        out.data_ptr(), q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs,
+        cos.data_ptr(), sin.data_ptr(), cs,
+        kv_cache.data_ptr(), num_blocks, h, hkv, bs, d, _DTYPES[kv_cache.dtype],
+        block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+        _ptr(cu_seqlens), context_lens.data_ptr(), n_seqs, n_tok, _stream(dev))
+    _lib.check(rc, "ndl_rope_kv_append")
+    return out
+
+
 def write_kv(k, v, kv_cache, block_table, cu_seqlens, context_lens) -> None:
     """Same signature and effect as the reference _write_kv (attention.py:204-246)."""
     kv_append(k, v, kv_cache, block_table, context_lens, cu_seqlens=cu_seqlens)

@@ -75,6 +75,15 @@ def test_rejections_before_any_launch(lib):
     rc = lib.ndl_paged_decode(None, None, 512, None, 1, None, 1, 1, None, 1, 4, 1, 128, 16, 0,
                               1.0, 24, None, 0, None)
     assert rc == -1
+    # rope_kv_append: fp16, a head_dim not a multiple of 16, null inputs
+    def rope(dtype=0, d=128, t=1, q=None):
+        return lib.ndl_rope_kv_append(None, q, 4 * d, None, d, None, d, None, None, d,
+                                      None, 1, 4, 1, 16, d, dtype, None, 1, 1, None, None, 1, t,
+                                      None)
+    assert rope(dtype=1) == -2
+    assert rope(d=72) == -2
+    assert rope(t=0) == 0
+    assert rope() == -1
     # nothing to do: zero tokens / sequences
     assert lib.ndl_kv_append(None, 1, 1, 16, 128, 0, None, 128, None, 128, None, 1, 1, None,
                              None, 1, 0, None) == 0

@@ -43,6 +43,7 @@ def _oracle_decode(self, q, k, v, kv_cache, block_table, context_lens):
 def oracle_runner(cfg, model_cpu):
     r = ModelRunner(cfg, device="cpu", model=model_cpu)
     for layer in r.model.model.layers:
+        layer.self_attn.fuse_rope = False       # RoPE as torch ops, then the oracle seams
         layer.self_attn._prefill = types.MethodType(_oracle_prefill, layer.self_attn)
         layer.self_attn._decode = types.MethodType(_oracle_decode, layer.self_attn)
     return r
