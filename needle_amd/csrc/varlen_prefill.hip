@@ -7,22 +7,30 @@
 // is the same data when context_lens == 0 and also covers a cached prefix.
 //
 // Design:
-//   * One workgroup = 8 waves = 128 query rows of one (sequence, query head);
-//     each wave owns 16 rows as the N columns of 16x16 MFMA tiles (other
-//     shapes are built for tuning: 4 waves x 16 or x 32 rows).
-//   * K/V advance 32 tokens (two cache blocks) per step through a 4-stage LDS
-//     ring filled by direct global->LDS loads (global_load_lds_dwordx4, no
-//     register staging): each instruction reads whole rows, 1 KiB contiguous,
-//     and lands them swizzled; three steps are in flight while one computes.
-//   * S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (A = K rows from LDS, B = Q^T
-//     held in registers).  Its accumulator layout is the B operand (P^T) of
-//     O^T = V^T P^T on the same instruction with a 32-token contraction whose
-//     k order interleaves the two blocks; V^T is assembled from LDS rows with
-//     the head_dim permutation d = (D/16) * m + b, so no cross-lane traffic.
-//   * fp32 online softmax (exp2, scale folded with log2 e); the causal mask is
-//     applied only on tiles that reach past a wave's first query position.
-//   * Query tiles are dispatched longest-first (the last tile of a sequence
-//     has the most keys).
+//   * One workgroup = one (sequence, kv head, 32-row query tile).  Its waves are
+//     the query heads of the GQA group (times 32-row subtiles when the group is
+//     small), so every K/V tile staged in LDS serves all g heads, and every wave
+//     of a workgroup has the same causal extent.
+//   * K/V advance 32 keys (two cache blocks) per step through an NS-stage LDS ring
+//     filled by direct global->LDS loads (global_load_lds_dwordx4, no register
+//     staging); each instruction reads whole rows, 1 KiB contiguous, and lands
+//     them with a row-dependent 16-byte chunk swizzle.
+//   * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: A = K rows from LDS
+//     (ds_read_b128), B = Q^T held in registers.  Lane l holds the scores of query
+//     row l%32 for 16 of the 32 keys, so a row max needs one permlane32 swap.
+//   * The S^T accumulator, rounded to bf16, is the B operand (P^T) of
+//     O^T = V^T P^T on the same instruction with the k order
+//     k = 8h + e -> key 16t + 4h + (e&3) + 8(e>>2); the matching V^T operand comes
+//     straight from LDS through ds_read_b64_tr_b16 (4 keys x 16 head_dim columns
+//     per 16 lanes), so P and V need no register shuffles.
+//   * Software pipeline: QK of step t+1 is issued before the softmax of step t,
+//     so the MFMA pipe works while the VALU computes exponentials.
+//   * fp32 online softmax in the exp2 domain (scale * log2 e folded into one FMA);
+//     the running max is only moved when a row's max grows by more than
+//     kRescaleSlack, so the O^T rescale is rare; the row sums are taken on the
+//     bf16-rounded P (v_dot2_f32_bf16), i.e. on what the PV product consumes.
+//   * Causal masking only on steps that reach past a wave's first query position;
+//     query tiles are dispatched longest-first.
 #include <stdlib.h>
 
 #include <type_traits>
@@ -31,8 +39,16 @@
 
 namespace ndl {
 
-constexpr int kPrefBlockN = 32;                               // keys per step (2 blocks)
-constexpr int kPrefStages = 4;                                // LDS ring depth (steps)
+constexpr int kPrefKeys = 32;          // keys per step (two cache blocks)
+constexpr int kPrefRows = 32;          // query rows per wave
+constexpr int kPrefMaxWaves = 8;       // waves per workgroup
+constexpr int kPrefLoaders = 4;        // waves that issue the ring's direct loads
+// Tile-list limits of the persistent launch (larger batches use one workgroup per tile).
+constexpr int kPrefListSeqs = 8192;
+constexpr int kPrefListLevels = 2048;
+// exp2-domain growth of a row max tolerated before the accumulator is rescaled:
+// probabilities stay <= 2^8, exact in bf16's exponent range and in fp32 sums.
+constexpr float kRescaleSlack = 8.0f;
 
 struct PrefillArgs {
   u16* out;
@@ -48,11 +64,19 @@ struct PrefillArgs {
   const int32_t* cu_seqlens;
   const int32_t* context_lens;
   int num_heads;
-  int group;
+  int group;          // query heads per kv head
+  int heads_per_wg;   // query heads one workgroup covers (a chunk of the group)
+  int head_chunks;    // workgroups per kv head along the group
+  int subtiles;       // 32-row subtiles per workgroup
   float scale_log2;
   int num_qtiles;
   int64_t num_tokens;
+  int num_seqs;
+  int persistent;     // 1: grid of resident workgroups walking the tile list
 };
+
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(4))) short i16x4v;
 
 // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding:
 // vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] at bits 15:14).
@@ -68,7 +92,7 @@ __device__ __forceinline__ void vm_wait() {
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "memory"); }
 
 // One direct global->LDS load: lane L reads 16 bytes at gbase + lane_off (gbase
-// wave-uniform) and they land at LDS byte lds_ptr + 16 * L.
+// wave-uniform) and they land at LDS byte address lds_addr + 16 * L (lds_addr uniform).
 // Issued from inline asm so the compiler does not order every later LDS read behind
 // it (it cannot tell the ring's stages apart); the ring waits on vmcnt itself.
 // M0 takes the LDS base; one wait state separates the M0 write from its use.  M0 is
@@ -78,288 +102,475 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "me
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void lds_dma16(const void* gbase, uint32_t lane_off,
-                                          const void* lds_ptr) {
-  const uint32_t base = __builtin_amdgcn_readfirstlane(
-      (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)lds_ptr);
+                                          uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
-               : "s"(base), "v"(lane_off), "s"(gbase)
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(lane_off), "s"(gbase)
                : "memory", "m0");
 }
 #pragma clang diagnostic pop
 
+// LDS byte address of a shared-memory pointer.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
+}
+
+// 16-byte chunk swizzle of a staged K row (row index within the 32-row stage).
+//   D = 128 (16 chunks per row): ((r & 3) << 2) | ((r >> 2) & 3)
+//   D = 64  (8 chunks per row):  (((r >> 1) & 1) << 2) | ((r >> 2) & 3)
+// Both keep the K operand read (16 consecutive rows at one chunk, ds_read_b128)
+// conflict-free.
 template <int D>
 __device__ __forceinline__ int pref_swz(int r) {
-  return D == 128 ? (r & 15) : ((r >> 1) & 7);
+  return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
 }
 
-// NB 16-row N-blocks per wave, WAVES waves per workgroup: 16 * NB * WAVES query rows.
-template <int D, int NB, int WAVES>
-__global__ __launch_bounds__(64 * WAVES) void varlen_prefill_kernel(PrefillArgs a) {
-  constexpr int KS = D / 32;          // k-steps of the QK MFMA
-  constexpr int DPL = D / 16;         // m-blocks of O^T (head_dim elements per lane per row)
+// Combine a value with the one held by lane l ^ 32 (v_permlane32_swap of a register
+// with itself: one result holds the lower half's values, the other the upper half's).
+__device__ __forceinline__ float half_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v),
+                                                  false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+template <int D, int NS>
+__global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(PrefillArgs a) {
+  constexpr int KS = D / 16;          // k-steps of the QK MFMA (16 head_dim each)
+  constexpr int DT = D / 32;          // 32-wide head_dim tiles of O^T
   constexpr int CPR = D / 8;          // 16-byte chunks per row
-  constexpr int kPrefRowsPerWave = 16 * NB;
-  constexpr int kPrefBlockM = kPrefRowsPerWave * WAVES;
-  constexpr int RPP = 512 / D;        // rows per 1 KiB piece (one direct load instruction)
-  constexpr int PIECES = 32 / RPP;    // pieces per plane per step
-  constexpr int IPW = 2 * PIECES / WAVES;  // direct load instructions per wave per step
-  static_assert(IPW >= 1 && (2 * PIECES) % WAVES == 0, "load distribution");
+  constexpr int RPP = 512 / D;        // rows per 1 KiB piece (one direct load)
+  constexpr int PIECES = kPrefKeys / RPP;                 // pieces per plane per step
+  constexpr int IPW = 2 * PIECES / kPrefLoaders;          // loads per loader wave per step
+  static_assert(IPW >= 1 && (2 * PIECES) % kPrefLoaders == 0, "load distribution");
+  static_assert(NS >= 3 && NS - 2 <= 6 && (NS - 2) * IPW < 64, "ring depth");
 
-  // Ring of kPrefStages steps; each stage holds 32 K rows and 32 V rows.
-  __shared__ __attribute__((aligned(16))) u16 lk[kPrefStages][32 * D];
-  __shared__ __attribute__((aligned(16))) u16 lv[kPrefStages][32 * D];
+  // Ring of NS steps; each stage holds 32 K rows and 32 V rows.
+  __shared__ __attribute__((aligned(16))) u16 lk[NS][kPrefKeys * D];
+  __shared__ __attribute__((aligned(16))) u16 lv[NS][kPrefKeys * D];
 
-  const int head = blockIdx.x;
-  const int qtile = a.num_qtiles - 1 - (int)blockIdx.y;  // longest tiles first
-  const int seq = blockIdx.z;
-  const int tid = threadIdx.x, lane = tid & 63, j = lane >> 4, c = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
+  const int hw = wave % a.heads_per_wg;                        // head within the chunk
+  const int sub = wave / a.heads_per_wg;                       // 32-row subtile
+  const int r32 = lane & 31, h = lane >> 5;
+  const int wg_rows = kPrefRows * a.subtiles;
 
-  // Rows past num_tokens are never touched, whatever cu_seqlens holds.
-  const int64_t tok0 = a.cu_seqlens[seq];
-  int64_t tok1 = a.cu_seqlens[seq + 1];
-  if (tok1 > a.num_tokens) tok1 = a.num_tokens;
-  if (tok0 < 0 || tok1 <= tok0) return;
-  const int n = (int)(tok1 - tok0);
-  const int row0 = qtile * kPrefBlockM;
-  if (row0 >= n) return;
-  const int ctx = a.context_lens[seq] < 0 ? 0 : a.context_lens[seq];
-  const int kvh = head / a.group;
-  const int kv_end = ctx + (row0 + kPrefBlockM < n ? row0 + kPrefBlockM : n);
-  const int nsteps = (kv_end + kPrefBlockN - 1) / kPrefBlockN;
+  // One query tile: rows qtile * wg_rows .. of sequence seq, kv head kvh, head chunk
+  // chunk.  Every wave of the workgroup runs it together (it has workgroup barriers).
+  auto tile = [&](const int seq, const int qtile, const int kvh, const int chunk) {
+    const int hg = chunk * a.heads_per_wg + hw;                  // head within the group
+    const int head = kvh * a.group + hg;
 
-  const int wrow0 = row0 + wave * kPrefRowsPerWave;           // first row of this wave
-  const int wlast = (wrow0 + kPrefRowsPerWave < n ? wrow0 + kPrefRowsPerWave : n) - 1;
-  const bool wave_active = wrow0 < n;
-  const int qpos_min = ctx + wrow0;                           // first query position
-  const int qpos_max = ctx + wlast;                           // last query position
+    // Rows past num_tokens are never touched, whatever cu_seqlens holds.
+    const int64_t tok0 = a.cu_seqlens[seq];
+    int64_t tok1 = a.cu_seqlens[seq + 1];
+    if (tok1 > a.num_tokens) tok1 = a.num_tokens;
+    if (tok0 < 0 || tok1 <= tok0) return;
+    const int n = (int)(tok1 - tok0);
+    const int row0 = qtile * wg_rows;
+    if (row0 >= n) return;
+    const int ctx = a.context_lens[seq] < 0 ? 0 : a.context_lens[seq];
+    const int kv_end = ctx + (row0 + wg_rows < n ? row0 + wg_rows : n);
+    const int nsteps = (kv_end + kPrefKeys - 1) / kPrefKeys;
 
-  // B operands of S^T = K Q^T: lane (j, c) supplies Q[row 16 nb + c][32 s + 8 j .. +8).
-  bf16x8 qb[NB][KS];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int row = wrow0 + 16 * nb + c;
-    const u16* qrow = a.q + (tok0 + row) * a.q_tok_stride + (int64_t)head * D + 8 * j;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      u32x4 w = row < n ? ld16(qrow + 32 * s) : u32x4{0u, 0u, 0u, 0u};
-      qb[nb][s] = __builtin_bit_cast(bf16x8, w);
-    }
-  }
-  // Retire the Q loads before the load ring starts, so that no wait inside the loop has
-  // to cover them (the ring's own waits count only its direct loads).
-  vm_wait<0>();
+    const int wrow0 = row0 + sub * kPrefRows;                    // first row of this wave
+    const bool wave_active = wrow0 < n && hg < a.group && sub < a.subtiles;
+    const int qpos_min = ctx + wrow0;
+    const int qpos = ctx + wrow0 + r32;                          // this lane's query position
 
-  const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
-  const int64_t head_off = (int64_t)kvh * 16 * D;
-  const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
-
-  // Block ids come from a 64-entry window of the table row held one per lane and are
-  // read with readlane (uniform).  A window refill waits for every outstanding load
-  // (a vector-memory wait cannot single one out); it happens once per 64 blocks.
-  int win0 = -64, btw = 0;
-  auto clamp_col = [&](int col) { return col > a.max_blocks - 1 ? a.max_blocks - 1 : col; };
-  uint32_t badbits = 0;  // bit 2*stage + b: block b of that stage's step is not a valid id
-
-  // Direct global->LDS loads.  Instruction p of a plane writes 1 KiB at piece p of the
-  // stage (lane L -> byte 16 L), i.e. row p*RPP + L/CPR at 16-byte slot L%CPR.  The
-  // slot must hold chunk slot ^ swz(row), so each lane fetches that chunk: every
-  // instruction still reads RPP whole rows, all inside one cache block, so the block
-  // base is uniform.  An invalid block id reads block 0 instead (always mapped); rows
-  // past the range read whatever the table maps them to.  compute() masks both.
-  auto issue = [&](int step) {
-    const int stage = step % kPrefStages;
-    const int c0 = clamp_col(2 * step), c1 = clamp_col(2 * step + 1);  // same 64-window
-    if (c0 < win0 || c0 >= win0 + 64) {
-      win0 = c0 & ~63;
-      btw = win0 + lane < a.max_blocks ? bt_row[win0 + lane] : 0;
-      vm_wait<0>();
-    }
-    const int64_t b0 = __builtin_amdgcn_readlane(btw, c0 - win0);
-    const int64_t b1 = __builtin_amdgcn_readlane(btw, c1 - win0);
-    const bool bad0 = b0 < 0 || b0 >= a.num_blocks, bad1 = b1 < 0 || b1 >= a.num_blocks;
-    badbits = (badbits & ~(3u << (2 * stage))) | ((bad0 ? 1u : 0u) << (2 * stage)) |
-              ((bad1 ? 2u : 0u) << (2 * stage));
-#pragma unroll
-    for (int e = 0; e < IPW; ++e) {
-      const int u = wave * IPW + e;                     // instruction index in the step
-      const bool vplane = u >= PIECES;
-      const int piece = vplane ? u - PIECES : u;
-      const int r0 = piece * RPP;                       // first row of the piece
-      const int64_t blk = r0 < 16 ? (bad0 ? 0 : b0) : (bad1 ? 0 : b1);
-      const int64_t row0 = blk * blk_stride + head_off + (int64_t)(r0 & 15) * D;
-      const int r = r0 + lane / CPR;
-      const uint32_t off = (uint32_t)(((lane / CPR) * D + 8 * ((lane % CPR) ^ pref_swz<D>(r))) * 2);
-      if (vplane)
-        lds_dma16(a.vplane + row0, off, &lv[stage][piece * 512]);
-      else
-        lds_dma16(a.kplane + row0, off, &lk[stage][piece * 512]);
-    }
-  };
-
-  f32x4 acc[NB][DPL];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-    for (int b = 0; b < DPL; ++b) acc[nb][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m[NB], lsum[NB];
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    m[nb] = kNegInf;
-    lsum[nb] = 0.f;
-  }
-
-  auto compute = [&](int step, int buf) {
-    const int kv0 = step * kPrefBlockN;
-    if (!wave_active || kv0 > qpos_max) return;  // every key of the step is in this wave's future
-    const bool diag = kv0 + kPrefBlockN - 1 > qpos_min;
-    // Keys of an invalid block are masked like future keys.
-    const bool bad0 = (badbits >> (2 * buf)) & 1u;
-    const bool bad1 = (badbits >> (2 * buf + 1)) & 1u;
-    const bool tail = kv0 + kPrefBlockN > kv_end;  // rows past the range hold stale bits
-    const bool masked = diag || bad0 || bad1 || tail;
-
-    // S^T for the two blocks and both N-blocks.
-    f32x4 st[2][NB];
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) st[blk][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int blk = 0; blk < 2; ++blk) {
-      const int r = 16 * blk + c;
+    // B operand of S^T = K Q^T: lane l supplies Q[row l%32][16 s + 8 h .. + 8).
+    bf16x8 qb[KS];
+    {
+      const int row = wrow0 + r32;
+      const bool ok = wave_active && row < n;
+      const u16* qrow = a.q + (tok0 + (ok ? row : 0)) * a.q_tok_stride + (int64_t)head * D + 8 * h;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        const u32x4 ka = *reinterpret_cast<const u32x4*>(
-            &lk[buf][r * D + 8 * ((j + 4 * s) ^ pref_swz<D>(r))]);
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          st[blk][nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-              __builtin_bit_cast(bf16x8, ka), qb[nb][s], st[blk][nb], 0, 0, 0);
+        u32x4 w = ok ? ld16(qrow + 16 * s) : u32x4{0u, 0u, 0u, 0u};
+        qb[s] = __builtin_bit_cast(bf16x8, w);
       }
     }
+    // Retire the Q loads before the ring starts, so that no wait inside the loop has to
+    // cover them (the ring's own waits count only its direct loads).
+    vm_wait<0>();
 
-    // V rows of this lane: e = 4 blk + i -> key 16 blk + 4 j + i, head_dim DPL*c .. +DPL.
-    using VT = typename std::conditional<D == 128, u32x4, u32x2>::type;
-    VT vrow[8];
+    const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
+    const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
+    // Block ids are int32; every id in [0, nb32) is a valid block.
+    const uint32_t nb32 = a.num_blocks > 0x7fffffff ? 0x80000000u : (uint32_t)a.num_blocks;
+
+    // Loader waves 0..3 stage, per step, plane (w >> 1) (K, V) of block (w & 1) of the
+    // step: IPW direct loads of 1 KiB each, into pieces (w & 1) * IPW + e of that plane.
+    //   K piece: RPP rows, row-major, LDS slot L%CPR of row L/CPR holding chunk
+    //     (L%CPR) ^ swz(row).
+    //   V piece e: the block's 16 rows at head_dim 32 e .. +32 ([row][32 d], 64 bytes
+    //     per row): lane L -> row L/4, chunk 4 e + L%4.
+    const bool loader = wave < kPrefLoaders;
+    const int ld_plane = wave >> 1, ld_blk = wave & 1;
+    const u16* ld_head = (ld_plane ? a.vplane : a.kplane) + (int64_t)kvh * 16 * D;
+    uint32_t ld_off[IPW];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int r = 16 * (e >> 2) + 4 * j + (e & 3);
-      if constexpr (D == 128) {
-        vrow[e] = *reinterpret_cast<const u32x4*>(&lv[buf][r * D + 8 * (c ^ pref_swz<D>(r))]);
+    for (int e = 0; e < IPW; ++e) {
+      if (ld_plane == 0) {
+        const int r0 = (ld_blk * IPW + e) * RPP;            // first row of the piece (stage)
+        const int r = r0 + lane / CPR;
+        ld_off[e] = (uint32_t)((((r0 & 15) + lane / CPR) * D +
+                                8 * ((lane % CPR) ^ pref_swz<D>(r))) * 2);
       } else {
-        vrow[e] = *reinterpret_cast<const u32x2*>(
-            &lv[buf][r * D + 8 * ((c >> 1) ^ pref_swz<D>(r)) + 4 * (c & 1)]);
-      }
-      if (masked) {  // stale rows may hold NaN bits: clear them (NaN * 0 = NaN)
-        const int kp = kv0 + r;
-        if (kp >= kv_end || ((e >> 2) ? bad1 : bad0)) vrow[e] = VT{};
+        ld_off[e] = (uint32_t)(((lane >> 2) * D + 32 * e + 8 * (lane & 3)) * 2);
       }
     }
+    const uint32_t lds_k0 = lds_addr(&lk[0][0]), lds_v0 = lds_addr(&lv[0][0]);
+    const uint32_t ld_lds = (ld_plane ? lds_v0 : lds_k0) + ld_blk * IPW * 1024;
 
-    bf16x8 pb[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int qpos = ctx + wrow0 + 16 * nb + c;
-      float sc[8];
-      float mt = kNegInf;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int blk = e >> 2, i = e & 3;
-        const int kp = kv0 + 16 * blk + 4 * j + i;
-        bool ok = true;
-        if (masked) ok = kp <= qpos && kp < kv_end && !(blk == 0 ? bad0 : bad1);
-        sc[e] = ok ? st[blk][nb][i] * a.scale_log2 : kNegInf;
-        mt = fmaxf(mt, sc[e]);
-      }
-      mt = fmaxf(mt, xor_shfl(mt, 16));
-      mt = fmaxf(mt, xor_shfl(mt, 32));
-      const float m_new = fmaxf(m[nb], mt);
-      const float m_use = m_new == kNegInf ? 0.f : m_new;
-      const float alpha = fast_exp2(m[nb] - m_use);
-      float p[8];
-      float ps = 0.f;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        p[e] = fast_exp2(sc[e] - m_use);
-        ps += p[e];
-      }
-      lsum[nb] = lsum[nb] * alpha + ps;
-      m[nb] = m_new;
-      if (__ballot(alpha != 1.f)) {  // rescale only when some row's max moved
-#pragma unroll
-        for (int b = 0; b < DPL; ++b) acc[nb][b] *= alpha;
-      }
-      pb[nb] = __builtin_bit_cast(
-          bf16x8, u32x4{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3]),
-                        pack_bf16x2(p[4], p[5]), pack_bf16x2(p[6], p[7])});
-    }
+    // Block ids come from a 64-entry window of the table row held one per lane and are
+    // read with readlane (uniform).  A window refill waits for every outstanding load
+    // (a vector-memory wait cannot single one out); it happens once per 64 blocks.
+    int win0 = -64, btw = 0;
+    auto clamp_col = [&](int col) { return col > a.max_blocks - 1 ? a.max_blocks - 1 : col; };
+    // bit 2*stage + b: block b of that stage's step is not a valid id.  Every wave keeps
+    // its own copy (all waves walk the same table window).
+    uint32_t badbits = 0;
 
-    // O^T += V^T P^T, one MFMA per (m-block, N-block).
+    // Stage `step` into ring slot `stage`: note its block validity and, on loader waves,
+    // issue its direct loads.  An invalid block id reads block 0 instead (always mapped);
+    // rows past the range read whatever the table maps them to.  The softmax masks both.
+    auto stage_in = [&](int step, int stage) {
+      const int c0 = clamp_col(2 * step), c1 = clamp_col(2 * step + 1);  // same 64-window
+      if (c0 < win0 || c0 >= win0 + 64) {
+        win0 = c0 & ~63;
+        btw = win0 + lane < a.max_blocks ? bt_row[win0 + lane] : 0;
+        vm_wait<0>();
+      }
+      const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane(btw, c0 - win0);
+      const uint32_t b1 = (uint32_t)__builtin_amdgcn_readlane(btw, c1 - win0);
+      const uint32_t bad = (b0 >= nb32 ? 1u : 0u) | (b1 >= nb32 ? 2u : 0u);
+      badbits = (badbits & ~(3u << (2 * stage))) | (bad << (2 * stage));
+      if (!loader) return;
+      const uint32_t b = ld_blk ? b1 : b0;
+      const u16* base = ld_head + (int64_t)(b < nb32 ? b : 0u) * blk_stride;
+      const uint32_t lds = ld_lds + (uint32_t)stage * (kPrefKeys * D * 2);
 #pragma unroll
-    for (int b = 0; b < DPL; ++b) {
-      uint32_t w[4];
-#pragma unroll
-      for (int h = 0; h < 4; ++h)
-        w[h] = pack_halves(vrow[2 * h][b >> 1], vrow[2 * h + 1][b >> 1], b & 1);
-      const bf16x8 va = __builtin_bit_cast(bf16x8, u32x4{w[0], w[1], w[2], w[3]});
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb)
-        acc[nb][b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[nb], acc[nb][b], 0, 0, 0);
-    }
-  };
+      for (int e = 0; e < IPW; ++e)
+        lds_dma16(base, ld_off[e], lds + 1024 * e);
+    };
 
-  // Main loop over a kPrefStages-deep ring: while step t computes, the direct loads of
-  // steps t+1 .. t+kPrefStages-1 are in flight.  One barrier per step: it publishes
-  // step t's loads and retires every wave's compute(t-1), whose stage step t reuses.
+    // Waits until this wave's loads of the step after the current one have landed:
+    // `later` = steps issued after it.
+    auto wait_loads = [&](int later) {
+      if (!loader) return;
+      switch (later) {
+        case 0: vm_wait<0>(); break;
+        case 1: vm_wait<IPW>(); break;
+        case 2: vm_wait<2 * IPW>(); break;
+        case 3: vm_wait<3 * IPW>(); break;
+        case 4: vm_wait<4 * IPW>(); break;
+        case 5: vm_wait<5 * IPW>(); break;
+        default: vm_wait<6 * IPW>(); break;
+      }
+    };
+
+    // Per-lane LDS element offsets of the operands inside a stage.
+    //   K (A of S^T = K Q^T), k-step s: row l%32, chunk 2s + h.
+    int koff[KS];
 #pragma unroll
-  for (int t = 0; t < kPrefStages - 1; ++t)
-    if (t < nsteps) issue(t);
-  for (int step = 0; step < nsteps; ++step) {
-    // Loads issued after step's own: min(kPrefStages - 2, nsteps - 1 - step) steps.
-    const int ahead = nsteps - 1 - step < kPrefStages - 2 ? nsteps - 1 - step : kPrefStages - 2;
-    if (ahead >= 2) vm_wait<2 * IPW>();
-    else if (ahead == 1) vm_wait<IPW>();
-    else vm_wait<0>();
+    for (int s = 0; s < KS; ++s) koff[s] = r32 * D + 8 * ((2 * s + h) ^ pref_swz<D>(r32));
+    // V^T operand (k-step t, head_dim tile dt, half k): the V piece (t, dt) holds rows
+    // 16t .. 16t+15 as [row][32 d]; lane (G = l/16, i = l%16) reads 4 elements of row
+    // 8k + 4h + i/4 at head_dim 16 (G&1) + 4 (i%4), and ds_read_b64_tr_b16 hands lane i
+    // column i of each of the 4 rows (keys 16t + 8k + 4h + x, x = 0..3).
+    const int vlane = (4 * h + ((lane & 15) >> 2)) * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+
+    f32x16 acc[DT];
+#pragma unroll
+    for (int t = 0; t < DT; ++t) acc[t] = f32x16{};
+    float m_run = kNegInf;   // running max of this lane's row (exp2 domain)
+    float l_run = 0.f;       // this lane's share of the row sum
+
+    // K operands of one stage (read ahead of the MFMAs that use them).
+    auto k_reads = [&](int stage, u32x4* ka) {
+      const u16* kt = lk[stage];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) ka[s] = *reinterpret_cast<const u32x4*>(&kt[koff[s]]);
+    };
+    // S^T of one step: st[r] = score of key 8(r/4) + 4h + r%4 for query row l%32.
+    auto qk = [&](const u32x4* ka) {
+      f32x16 st = {};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[s]), qb[s], st,
+                                                     0, 0, 0);
+      return st;
+    };
+    // P = exp2(s * scale log2e - m) rounded to bf16 (the B operand of the PV product);
+    // the row sum accumulates the rounded values.
+    auto probs = [&](const f32x16& st, float m_use, uint32_t* pw) {
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(fmaf(st[r], a.scale_log2, -m_use));
+        const float p1 = fast_exp2(fmaf(st[r + 1], a.scale_log2, -m_use));
+        pw[r >> 1] = pack_bf16x2(p0, p1);
+        l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[r >> 1]),
+                                                bf16x2{(__bf16)1.0f, (__bf16)1.0f}, l_run, false);
+      }
+    };
+    // O^T += V^T P^T over the step's 32 keys.
+    auto pv = [&](int stage, const uint32_t* pw) {
+      const u16* vt = lv[stage] + vlane;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pw[4 * t], pw[4 * t + 1],
+                                                           pw[4 * t + 2], pw[4 * t + 3]});
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt) {
+          const u16* piece = vt + (t * DT + dt) * 512;
+          const i16x4v v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4v*)(piece));
+          const i16x4v v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4v*)(piece + 8 * 32));
+          const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
+          const bf16x8 vop = __builtin_bit_cast(bf16x8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pb, acc[dt], 0, 0, 0);
+        }
+      }
+    };
+
+    // V rows past the range or in an invalid block may hold any bits, NaN included, and
+    // NaN * 0 = NaN in the PV product: a step with such rows has them cleared in LDS once
+    // its loads have landed (one barrier before its PV).  Only a workgroup's last step
+    // and steps over invalid block ids need this.
+    auto needs_vzero = [&](int step, int stage) {
+      return step * kPrefKeys + kPrefKeys > kv_end || ((badbits >> (2 * stage)) & 3u) != 0;
+    };
+    auto zero_v = [&](int step, int stage) {
+      const int kv0 = step * kPrefKeys;
+      int valid[2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int v = (badbits >> (2 * stage + t)) & 1u ? 0 : kv_end - (kv0 + 16 * t);
+        valid[t] = v < 0 ? 0 : (v > 16 ? 16 : v);
+      }
+      // 16-byte chunk c of the stage's V plane: piece c / 64 (t = piece / DT), row (c % 64) / 4
+      for (int c = tid; c < 2 * DT * 64; c += blockDim.x) {
+        const int piece = c >> 6, row = (c & 63) >> 2;
+        if (row >= valid[piece / DT]) st16(&lv[stage][c * 8], u32x4{0u, 0u, 0u, 0u});
+      }
+    };
+
+    // One iteration of the ring: QK(step + 1) and the softmax + PV of step.  Its barrier
+    // publishes step+1's loads and retires every wave's previous iteration (the last
+    // reader of slot (step - 1) % NS), which then takes step + NS - 1.
+    //   Fast path (no key of the step masked for this wave, no row max moved past the
+    //   slack): one straight-line block, so the QK MFMAs of step+1 interleave with the
+    //   exponentials of step.  Otherwise the slow path masks, rescales, then does the same.
+    //   QK of a step past the last one reads a stale slot; its scores are never used.
+    auto iteration = [&](int step, int stage, f32x16& st_cur, f32x16& st_next) {
+      const int nstage = stage + 1 == NS ? 0 : stage + 1;
+      const bool has_next = step + 1 < nsteps;
+      // loads of steps issued after step + 1: min(NS - 3, nsteps - 2 - step)
+      if (has_next) wait_loads(nsteps - 2 - step < NS - 3 ? nsteps - 2 - step : NS - 3);
+      lds_barrier();
+      if (step + NS - 1 < nsteps) stage_in(step + NS - 1, stage == 0 ? NS - 1 : stage - 1);
+      if (has_next && needs_vzero(step + 1, nstage)) zero_v(step + 1, nstage);
+      const int kv0 = step * kPrefKeys;
+      const bool masked = kv0 + kPrefKeys - 1 > qpos_min || kv0 + kPrefKeys > kv_end ||
+                          ((badbits >> (2 * stage)) & 3u) != 0;
+      f32x16 st = st_cur;
+      if (masked) {
+        const bool bad0 = (badbits >> (2 * stage)) & 1u;
+        const bool bad1 = (badbits >> (2 * stage + 1)) & 1u;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = 8 * (r >> 2) + 4 * h + (r & 3);
+          const int kp = kv0 + key;
+          const bool ok = kp <= qpos && kp < kv_end && !(key < 16 ? bad0 : bad1);
+          st[r] = ok ? st[r] : kNegInf;
+        }
+      }
+      float mx = fmaxf(fmaxf(st[0], st[1]), st[2]);
+#pragma unroll
+      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, st[r]), st[r + 1]);
+      mx = fmaxf(mx, st[15]);
+      mx = half_max(mx);
+      const float mx2 = mx * a.scale_log2;
+      const bool grow = mx2 > m_run + kRescaleSlack;
+      uint32_t pw[8];
+      u32x4 ka[KS];
+      if (!masked && __builtin_amdgcn_ballot_w64(grow) == 0) {
+        k_reads(nstage, ka);
+        probs(st, m_run, pw);
+        st_next = qk(ka);
+        pv(stage, pw);
+      } else {
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float m_new = grow ? mx2 : m_run;
+          // 0 when m_run is -inf; rows whose max stays put keep their scale exactly.
+          // In place (tied asm operands): a plain multiply lets the register allocator give
+          // the scaled accumulator new registers and copy it back on every step.
+          const float alpha = m_new == m_run ? 1.f : fast_exp2(m_run - m_new);
+#pragma unroll
+          for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+              asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
+          l_run *= alpha;
+          m_run = m_new;
+        }
+        k_reads(nstage, ka);
+        probs(st, m_run == kNegInf ? 0.f : m_run, pw);
+        st_next = qk(ka);
+        pv(stage, pw);
+      }
+    };
+
+    // Ring: steps 0 .. NS-2 in flight at the start; the loop is unrolled by two so that
+    // the two score tiles alternate without copies.  The barrier retires every wave's
+    // reads of the previous tile (persistent launch) before the slots are refilled.
     lds_barrier();
-    if (step + kPrefStages - 1 < nsteps) issue(step + kPrefStages - 1);
-    compute(step, step % kPrefStages);
+#pragma unroll
+    for (int t = 0; t < NS - 1; ++t)
+      if (t < nsteps) stage_in(t, t);
+    wait_loads(nsteps - 1 < NS - 2 ? nsteps - 1 : NS - 2);
+    lds_barrier();
+    if (needs_vzero(0, 0)) zero_v(0, 0);
+    f32x16 st0, st1;
+    {
+      u32x4 ka[KS];
+      k_reads(0, ka);
+      st0 = qk(ka);
+    }
+    int step = 0, stage = 0;
+    for (; step + 2 <= nsteps; step += 2) {
+      iteration(step, stage, st0, st1);
+      stage = stage + 1 == NS ? 0 : stage + 1;
+      iteration(step + 1, stage, st1, st0);
+      stage = stage + 1 == NS ? 0 : stage + 1;
+    }
+    if (step < nsteps) iteration(step, stage, st0, st1);
+
+    if (!wave_active) return;
+    const int row = wrow0 + r32;
+    const float l = half_sum(l_run);
+    if (row >= n) return;
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+    // acc[dt][r] holds O[row][d = 32 dt + 8 (r/4) + 4 h + r%4].
+    u16* dst = a.out + ((tok0 + row) * a.num_heads + head) * (int64_t)D + 4 * h;
+#pragma unroll
+    for (int dt = 0; dt < DT; ++dt)
+#pragma unroll
+      for (int b = 0; b < 4; ++b)
+        *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * b) =
+            u32x2{pack_bf16x2(acc[dt][4 * b] * inv, acc[dt][4 * b + 1] * inv),
+                  pack_bf16x2(acc[dt][4 * b + 2] * inv, acc[dt][4 * b + 3] * inv)};
+  };  // tile
+
+  if (!a.persistent) {
+    tile(blockIdx.y, a.num_qtiles - 1 - (int)blockIdx.z, blockIdx.x / a.head_chunks,
+         blockIdx.x % a.head_chunks);
+    return;
   }
 
-  if (!wave_active) return;
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    float l = lsum[nb];
-    l += xor_shfl(l, 16);
-    l += xor_shfl(l, 32);
-    const int row = wrow0 + 16 * nb + c;
-    if (row >= n) continue;
-    const float inv = l > 0.f ? 1.f / l : 0.f;
-    // acc[nb][b][i] holds O[row][d = DPL * (4 j + i) + b].
-    u16* dst = a.out + ((tok0 + row) * a.num_heads + head) * (int64_t)D + DPL * 4 * j;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t w[DPL / 2];
-#pragma unroll
-      for (int b = 0; b < DPL; b += 2)
-        w[b / 2] = pack_bf16x2(acc[nb][b][i] * inv, acc[nb][b + 1][i] * inv);
-      if constexpr (DPL == 8)
-        st16(dst + DPL * i, u32x4{w[0], w[1], w[2], w[3]});
-      else
-        *reinterpret_cast<u32x2*>(dst + DPL * i) = u32x2{w[0], w[1]};
+  // Persistent launch: every workgroup builds the same tile list in LDS, longest tiles
+  // first (level t = query tile index, from the last down to 0; within a level the
+  // sequences that reach it, ascending, times the kv-head chunks), then takes items
+  // w, 2G-1-w, 2G+w, 4G-1-w, ... (G workgroups).  Query tiles past max_seqlen are not
+  // computed, as in the one-workgroup-per-tile launch.
+  __shared__ uint16_t s_ntiles[kPrefListSeqs];
+  __shared__ int s_cnt[kPrefListLevels];    // sequences with more than t tiles
+  __shared__ int s_off[kPrefListLevels];    // items in the levels above t
+  const int S = a.num_seqs, NQ = a.num_qtiles, KVC = a.num_kv_heads * a.head_chunks;
+  for (int t = tid; t < NQ; t += blockDim.x) s_cnt[t] = 0;
+  lds_barrier();
+  for (int q = tid; q < S; q += blockDim.x) {
+    const int64_t t0 = a.cu_seqlens[q];
+    int64_t t1 = a.cu_seqlens[q + 1];
+    if (t1 > a.num_tokens) t1 = a.num_tokens;
+    int nt = 0;
+    if (t0 >= 0 && t1 > t0) {
+      const int64_t x = (t1 - t0 + wg_rows - 1) / wg_rows;
+      nt = x > NQ ? NQ : (int)x;
     }
+    s_ntiles[q] = (uint16_t)nt;
+    if (nt > 0) atomicAdd(&s_cnt[nt - 1], 1);
+  }
+  lds_barrier();
+  if (wave == 0) {  // suffix sums: s_cnt[t] = #seqs with ntiles > t; s_off[t] = items above t
+    int run_cnt = 0, run_items = 0;
+    for (int base = NQ - 1; base >= 0; base -= 64) {
+      const int t = base - lane;
+      const int hcount = t >= 0 ? s_cnt[t] : 0;
+      // inclusive prefix over lanes 0..lane (descending t)
+      int inc = hcount;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(inc, d, 64);
+        if (lane >= d) inc += o;
+      }
+      const int cnt = run_cnt + inc;                 // seqs with ntiles > t
+      int inc_items = cnt;
+#pragma unroll
+      for (int d = 1; d < 64; d <<= 1) {
+        const int o = __shfl_up(inc_items, d, 64);
+        if (lane >= d) inc_items += o;
+      }
+      if (t >= 0) {
+        s_cnt[t] = cnt;
+        s_off[t] = (run_items + inc_items - cnt) * KVC;
+      }
+      run_cnt = __shfl(cnt, 63, 64);
+      run_items += __shfl(inc_items, 63, 64);
+    }
+  }
+  lds_barrier();
+  const int total = NQ > 0 ? s_off[0] + s_cnt[0] * KVC : 0;
+  const int G = gridDim.x, w = blockIdx.x;
+  int lvl = NQ - 1;
+  for (int r = 0; r * G < total; ++r) {
+    const int j = (r & 1) ? r * G + (G - 1 - w) : r * G + w;
+    if (j >= total) continue;
+    while (j >= s_off[lvl] + s_cnt[lvl] * KVC) --lvl;        // j only grows
+    const int i = j - s_off[lvl];
+    int rank = i / KVC;
+    const int c = i - rank * KVC;
+    int seq = -1;
+    for (int base = 0; base < S && seq < 0; base += 64) {
+      const int q = base + lane;
+      const uint64_t m = __builtin_amdgcn_ballot_w64(q < S && s_ntiles[q] > lvl);
+      const int pc = __builtin_popcountll(m);
+      if (rank < pc) {
+        uint64_t mm = m;
+        for (int k = 0; k < rank; ++k) mm &= mm - 1;       // drop the lowest `rank` bits
+        seq = base + __builtin_ctzll(mm);
+      } else {
+        rank -= pc;
+      }
+    }
+    tile(seq, lvl, c / a.head_chunks, c % a.head_chunks);
   }
 }
 
-// Workgroup shape (see the launch below).  NDL_PREFILL_VARIANT overrides it for tuning.
-inline int prefill_variant() {
-  static const int v = [] {
-    const char* e = getenv("NDL_PREFILL_VARIANT");
-    const int x = e ? atoi(e) : 2;
-    return (x >= 0 && x <= 2) ? x : 2;
-  }();
-  return v;
+// Workgroups of `fn` that can be resident at once on the current device (CUs times
+// workgroups per CU), cached per device and block size.
+inline int resident_slots(const void* fn, int block) {
+  struct Entry { const void* fn; int block; int dev; int slots; };
+  static Entry cache[32];
+  static int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return -1;
+  for (int i = 0; i < used; ++i)
+    if (cache[i].fn == fn && cache[i].block == block && cache[i].dev == dev) return cache[i].slots;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, 0) != hipSuccess)
+    return -1;
+  const int slots = cus * (per_cu > 0 ? per_cu : 1);
+  if (used < 32) cache[used++] = Entry{fn, block, dev, slots};
+  return slots;
 }
 
 }  // namespace ndl
@@ -386,11 +597,21 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
     return NDL_ERR_INVALID_ARG;
   if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)kv_cache) & 15u) return NDL_ERR_INVALID_ARG;
   if (q_tok_stride & 7) return NDL_ERR_INVALID_ARG;
-  const int variant = prefill_variant();
-  const int block_m = variant == 0 ? 128 : variant == 1 ? 64 : 128;
-  const int64_t qtiles = ((int64_t)max_seqlen + block_m - 1) / block_m;
-  if (num_seqs > 65535 || qtiles > 65535) return NDL_ERR_UNSUPPORTED;
   (void)max_context_len;
+
+  // Workgroup shape: the group's query heads (in chunks of at most 8), times 32-row
+  // subtiles while that stays within 8 waves; at least kPrefLoaders waves.
+  const int group = num_heads / num_kv_heads;
+  const int chunks = (group + kPrefMaxWaves - 1) / kPrefMaxWaves;
+  const int hpw = (group + chunks - 1) / chunks;
+  int subtiles = kPrefMaxWaves / hpw;
+  if (subtiles < 1) subtiles = 1;
+  int waves = hpw * subtiles;
+  if (waves < kPrefLoaders) waves = kPrefLoaders;
+  const int wg_rows = kPrefRows * subtiles;
+  const int64_t qtiles = ((int64_t)max_seqlen + wg_rows - 1) / wg_rows;
+  const int64_t gx = (int64_t)num_kv_heads * chunks;
+  if (num_seqs > 65535 || qtiles > 65535 || gx > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
 
   PrefillArgs a;
   a.out = (u16*)out;
@@ -406,28 +627,32 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
   a.cu_seqlens = cu_seqlens;
   a.context_lens = context_lens;
   a.num_heads = num_heads;
-  a.group = num_heads / num_kv_heads;
+  a.group = group;
+  a.heads_per_wg = hpw;
+  a.head_chunks = chunks;
+  a.subtiles = subtiles;
   a.scale_log2 = scale * kLog2e;
   a.num_qtiles = (int)qtiles;
   a.num_tokens = num_tokens;
 
-  const dim3 grid((unsigned)num_heads, (unsigned)qtiles, (unsigned)num_seqs);
   hipStream_t s = (hipStream_t)stream;
-  // variant 0: 4 waves x 32 rows; 1: 4 waves x 16 rows; 2: 8 waves x 16 rows.
-  if (head_dim == 128) {
-    if (variant == 1)
-      hipLaunchKernelGGL((varlen_prefill_kernel<128, 1, 4>), grid, dim3(256), 0, s, a);
-    else if (variant == 2)
-      hipLaunchKernelGGL((varlen_prefill_kernel<128, 1, 8>), grid, dim3(512), 0, s, a);
-    else
-      hipLaunchKernelGGL((varlen_prefill_kernel<128, 2, 4>), grid, dim3(256), 0, s, a);
-  } else {
-    if (variant == 1)
-      hipLaunchKernelGGL((varlen_prefill_kernel<64, 1, 4>), grid, dim3(256), 0, s, a);
-    else if (variant == 2)
-      hipLaunchKernelGGL((varlen_prefill_kernel<64, 1, 8>), grid, dim3(512), 0, s, a);
-    else
-      hipLaunchKernelGGL((varlen_prefill_kernel<64, 2, 4>), grid, dim3(256), 0, s, a);
+  // Persistent launch (one resident workgroup per slot, walking the longest-first tile
+  // list) unless the list would not fit in LDS.
+  a.num_seqs = num_seqs;
+  a.persistent = num_seqs <= kPrefListSeqs && qtiles <= kPrefListLevels &&
+                 gx * (int64_t)num_seqs * qtiles < ((int64_t)1 << 31);
+  const void* fn = head_dim == 128 ? (const void*)varlen_prefill_kernel<128, 5>
+                                   : (const void*)varlen_prefill_kernel<64, 8>;
+  dim3 grid((unsigned)gx, (unsigned)num_seqs, (unsigned)qtiles);
+  if (a.persistent) {
+    const int slots = resident_slots(fn, 64 * waves);
+    if (slots <= 0) return NDL_ERR_LAUNCH;
+    const int64_t items = gx * (int64_t)num_seqs * qtiles;   // upper bound of the list
+    grid = dim3((unsigned)(items < slots ? items : slots), 1, 1);
   }
+  if (head_dim == 128)
+    hipLaunchKernelGGL((varlen_prefill_kernel<128, 5>), grid, dim3(64 * waves), 0, s, a);
+  else
+    hipLaunchKernelGGL((varlen_prefill_kernel<64, 8>), grid, dim3(64 * waves), 0, s, a);
   return check_launch();
 }

@@ -76,7 +76,8 @@ def test_qwen2_7b_prefill_sampled_rows_vs_fp64():
 
 @pytest.mark.parametrize("shape", [
     wl.QWEN2_7B, wl.LLAMA3_8B, wl.QWEN2_05B, wl.HeadShape(8, 8, 128), wl.HeadShape(16, 2, 128),
-    wl.HeadShape(8, 1, 64), wl.HeadShape(12, 4, 64)])
+    wl.HeadShape(8, 1, 64), wl.HeadShape(12, 4, 64), wl.HeadShape(16, 1, 128),
+    wl.HeadShape(18, 2, 64)])
 def test_shapes_and_edge_lengths(shape):
     lens = [1, 15, 16, 17, 31, 32, 33, 127, 128, 129, 300]
     case = wl.prefill_case(shape, lens, seed=301)
@@ -111,4 +112,40 @@ def test_allocator_tables_and_many_prompts():
     case = wl.prefill_case(shape, lens, seed=304, table="allocator")
     got, _ = run_gpu(case)
     want, _ = oracle(case)
+    assert_close(got, want)
+
+
+def test_invalid_block_ids_are_masked():
+    """A block id outside [0, num_blocks) is never dereferenced: append skips its rows and
+    attention drops its keys (a row left with no valid key returns zeros)."""
+    shape = wl.QWEN2_7B
+    case = wl.prefill_case(shape, [40, 70, 20], seed=305)
+    nb = case.kv_cache.shape[1]
+    bt = case.block_table.clone()
+    bt[0, 1] = -3          # positions 16..31 of prompt 0
+    bt[1, 2] = nb + 7      # positions 32..47 of prompt 1
+    bt[2, 0] = -1          # positions 0..15 of prompt 2: rows 0..15 see no valid key
+    case.block_table = bt
+    got, pool = run_gpu(case)
+    s = case.shape
+    g = s.group
+    kvn = pool.double().numpy()
+    qn = case.q.double().numpy()
+    btl = bt.tolist()
+    cu = case.cu_seqlens.tolist()
+    want = np.zeros(got.shape)
+    for i in range(len(cu) - 1):
+        w = len(btl[i])
+        for t in range(cu[i], cu[i + 1]):
+            p = t - cu[i]
+            keys = [j for j in range(p + 1) if 0 <= btl[i][min(j // 16, w - 1)] < nb]
+            for h in range(s.num_heads):
+                if not keys:
+                    continue
+                kvh = h // g
+                kr = np.stack([kvn[0, btl[i][min(j // 16, w - 1)], kvh, j % 16] for j in keys])
+                vr = np.stack([kvn[1, btl[i][min(j // 16, w - 1)], kvh, j % 16] for j in keys])
+                sc = kr @ qn[t, h] * s.scale
+                pr = np.exp(sc - sc.max())
+                want[t, h] = pr @ vr / pr.sum()
     assert_close(got, want)
