@@ -10,12 +10,17 @@ HBM).  One step = for each of the 32 layers: append one new K/V token per
 sequence, then paged decode attention over block_table.
 
 Printed (one JSON line):
-  value         algorithmic bytes of the whole step / step time   (GB/s)
-  roofline      paged decode alone: algorithmic bytes per launch / average
-                launch time, timed with events on the launch stream, vs the
-                8 TB/s HBM peak
+  value         algorithmic bytes of the whole step / step time   (GB/s); the step is
+                captured once as a HIP graph and replayed, as a serving loop replays its
+                decode steps (ms_per_step_eager: the same step launched from Python)
+  roofline      paged decode alone (attention + partition merge): algorithmic bytes per
+                launch / average launch time over graph replays of the 32 layers, timed
+                with events on the launch stream, vs the 8 TB/s HBM peak
   cpu_baseline  the CPU restatement of the reference torch path, one layer
                 of the same workload, on this host's cores
+  other_shapes  Qwen2-0.5B layer decode, Qwen2-7B varlen prefill, Llama-3-8B long-context
+                decode, and end-to-end continuous batching on random-init Qwen2-0.5B
+                (output tokens/s, the reference benchmark's definition)
 Algorithmic bytes: every attended K/V row once, q in, output out, the block
 table entries and context lengths read; for append, k/v rows read and
 written plus their slot indices.
@@ -46,6 +51,9 @@ def parse_args():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-extras", action="store_true",
                    help="skip the Qwen2-0.5B, Qwen2-7B prefill and long-context measurements")
+    p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine run")
+    p.add_argument("--e2e-seconds", type=float, default=120.0,
+                   help="time limit of the end-to-end run (it finishes in about 30 s)")
     p.add_argument("--profile", action="store_true",
                    help="counter-collection driver: --steps steps of the workload, then three "
                         "1 GiB device copies (the calibration kernel), no timing output")
@@ -102,6 +110,41 @@ def time_region(torch, fn, reps):
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
+
+
+def capture(torch, fn):
+    """fn() captured as a HIP graph (after one eager call on a side stream to settle it)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def e2e_measurement(torch, time_limit_s):
+    """Continuous batching on random-init Qwen2-0.5B (the reference's benchmark definition:
+    generated tokens / wall time of the step loop after every request is submitted)."""
+    from needle_amd import e2e
+    t0 = time.perf_counter()
+    engine = e2e.build_engine()
+    build_s = time.perf_counter() - t0
+    reqs = e2e.requests()
+    n_tok, secs, finished = e2e.run(engine, reqs, sync=torch.cuda.synchronize,
+                                    time_limit_s=time_limit_s)
+    del engine
+    torch.cuda.empty_cache()
+    return {"output_tok_per_s": round(n_tok / secs, 1), "output_tokens": n_tok,
+            "seconds": round(secs, 2), "requests_finished": finished, "requests": len(reqs),
+            "engine_build_s": round(build_s, 1),
+            "workload": "random-init Qwen2-0.5B (24 layers, hidden 896, 14/2 heads), 256 "
+                        "requests, prompt U[64,1024], greedy output U[128,512], scheduler "
+                        "256 seqs / 8192 tokens, decode steps replayed from HIP graphs"}
 
 
 def extra_measurements(torch, ops, wl, reps):
@@ -249,9 +292,14 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    ms_step = time_region(torch, step, args.steps)
+    ms_step_eager = time_region(torch, step, args.steps)
 
-    # per-op timings over the same rotating pools
+    # The same step captured once as a HIP graph and replayed, as a serving loop runs
+    # its decode steps (host launch overhead out of the timed region).
+    g_step = capture(torch, step)
+    ms_step = time_region(torch, g_step.replay, args.steps)
+
+    # per-op timings over the same rotating pools, each a graph of its 32 launches
     def decode_all():
         for l in range(LAYERS):
             decode_layer(l)
@@ -260,8 +308,10 @@ def main():
         for l in range(LAYERS):
             append_layer(l)
 
-    ms_dec = time_region(torch, decode_all, args.steps) / LAYERS
-    ms_app = time_region(torch, append_all, args.steps) / LAYERS
+    g_dec, g_app = capture(torch, decode_all), capture(torch, append_all)
+    ms_dec = time_region(torch, g_dec.replay, args.steps) / LAYERS
+    ms_app = time_region(torch, g_app.replay, args.steps) / LAYERS
+    del g_step, g_dec, g_app
 
     dec_b = wl.decode_bytes(shape, ctx, width)
     app_b = wl.append_bytes(shape, len(ctx), len(ctx), varlen=False)
@@ -277,6 +327,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
+        "ms_per_step_eager": round(ms_step_eager, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -299,12 +350,16 @@ def main():
             "algorithmic_bytes_per_launch": dec_b, "avg_launch_us": round(ms_dec * 1e3, 2),
         },
         "kv_append": {"achieved_gbs": round(app_gbs, 1), "avg_launch_us": round(ms_app * 1e3, 2),
-                      "algorithmic_bytes_per_launch": app_b},
+                      "algorithmic_bytes_per_launch": app_b,
+                      "note": "64 rows per launch: latency-bound, not an HBM-bandwidth figure"},
     }
     if not args.no_extras:
         del pools
         torch.cuda.empty_cache()
         result["other_shapes"] = extra_measurements(torch, ops, wl, max(args.steps // 5, 5))
+    if not args.no_e2e:
+        result.setdefault("other_shapes", {})["qwen2_0.5b_e2e_continuous_batching"] = \
+            e2e_measurement(torch, args.e2e_seconds)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, wl, shape, ctx, args.cpu_seconds)
     print(json.dumps(result), flush=True)
