@@ -258,7 +258,8 @@ def main():
     (shape, ctx, tables, num_blocks, bt, ctx_t, pools, qs, ks, vs,
      outs) = build_workload(torch, wl, dev)
     width = bt.shape[1]
-    ws_bytes = ops.decode_workspace_bytes(len(ctx), shape.num_heads, shape.head_dim, width,
+    ws_bytes = ops.decode_workspace_bytes(len(ctx), shape.num_heads, shape.num_kv_heads,
+                                          shape.head_dim, width,
                                           shape.block_size, args.partition)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
     h, hkv, d, sc = shape.num_heads, shape.num_kv_heads, shape.head_dim, shape.scale

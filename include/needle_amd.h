@@ -44,7 +44,7 @@ extern "C" {
 /* Same object as hipStream_t; declared here so callers need no HIP headers. */
 typedef struct ihipStream_t* ndl_stream_t;
 
-#define NDL_ABI_VERSION 1
+#define NDL_ABI_VERSION 2
 
 enum ndl_status {
   NDL_OK = 0,
@@ -119,11 +119,13 @@ int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stride,
                        int num_seqs, int64_t num_tokens, ndl_stream_t stream);
 
 /*
- * Bytes of scratch ndl_paged_decode needs for this shape.  partition_tokens
- * = 0 selects the built-in default; pass the same value to ndl_paged_decode.
+ * Bytes of scratch ndl_paged_decode needs for this shape (a fixed function of the
+ * arguments, 0 for an invalid shape).  partition_tokens = 0 selects the built-in
+ * split; a multiple of 16 asks for that many tokens per wave.  Pass the same value
+ * to ndl_paged_decode.
  */
-size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
-                                        int max_blocks_per_seq, int block_size,
+size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
+                                        int head_dim, int max_blocks_per_seq, int block_size,
                                         int partition_tokens);
 
 /*
@@ -140,7 +142,8 @@ size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_di
  * q: [num_seqs][num_heads][head_dim], token stride q_tok_stride.
  * out: [num_seqs][num_heads][head_dim] contiguous.  fp32 accumulation.
  * L_i <= 0 gives zeros.  Supported: bf16, block_size 16, head_dim 64 or 128,
- * num_heads / num_kv_heads in 1..16.
+ * num_heads / num_kv_heads in 1..16.  The workspace (ndl_paged_decode_workspace_bytes)
+ * is always required; calls that share one must not overlap.
  */
 int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
                      const void* kv_cache, int64_t num_blocks,

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 _PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = _PKG_DIR / "libneedle_amd.so"
 
-NDL_ABI_VERSION = 1
+NDL_ABI_VERSION = 2
 NDL_DTYPE_BF16 = 0
 NDL_DTYPE_F16 = 1
 
@@ -53,7 +53,7 @@ _SIGNATURES = {
         _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
         _c_p, _c_p, _c_i32, _c_i64, _c_p,               # cu, ctx, B, T, stream
     ]),
-    "ndl_paged_decode_workspace_bytes": (_c_sz, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "ndl_paged_decode_workspace_bytes": (_c_sz, [_c_i32] * 7),
     "ndl_paged_decode": (_c_i32, [
         _c_p, _c_p, _c_i64,                             # out, q, q stride
         _c_p, _c_i64,                                   # cache, NB

@@ -3,12 +3,23 @@
 // Reference: needle/layers/attention.py:291-310 (_decode_pytorch): per
 // sequence gather K/V blocks, expand the GQA group, softmax(q K^T * scale) V.
 //
-// Design (one wave64 per (sequence, kv head, context partition)):
+// Work split (stream-K): for each kv head, the 16-token tiles of all sequences are
+// laid end to end (sequence i owns tiles P_i .. P_i + n_i, n_i = ceil(L_i / 16)),
+// and wave s of the kv head takes the C consecutive tiles s*C .. s*C + C, whatever
+// sequences they belong to.  Every wave has the same amount of K/V to stream, so
+// all of them run for the whole launch (a per-sequence split leaves the waves of
+// short remainders idle while the long ones finish).  The (wave s, sequence i)
+// piece of a sequence that spans waves leaves partial (m, l, unnormalised acc) in
+// segment slot s + i of its kv head (unique: the waves and the sequences are both
+// in stream order); a sequence inside one wave is written directly.  A wave finds
+// its first sequence with a wave-parallel prefix scan of context_lens.
+//
+// Per tile (one wave64):
 //   * The g query heads of a kv head are the N columns (padded to 16) of a
 //     16x16 MFMA tile; the 16 tokens of one cache block are its M rows.
-//     S^T = K . Q^T runs as head_dim/32 v_mfma_f32_16x16x32_bf16 steps whose
-//     A operand is read straight from the block (lane = token row, 16 bytes
-//     of head_dim per lane) -- no LDS, no conversion.
+//     S^T = K . Q^T runs as head_dim/32 v_mfma_f32_16x16x32_bf16 steps; K is
+//     fetched in row layout (1 KiB contiguous per load instruction), staged in a
+//     swizzled 4 KiB LDS tile and read back in the A-operand layout.
 //   * The S^T accumulator layout (lane 16j+c holds tokens 4j..4j+3 of head c)
 //     is exactly the B operand layout of v_mfma_f32_16x16x16bf16_1k, so
 //     P^T feeds O^T = V^T . P^T without any cross-lane movement.  V^T is the
@@ -17,17 +28,16 @@
 //     elements of a V row and only repacks registers.
 //   * Online softmax in fp32 with exp2 (scale folded with log2 e).  The row
 //     max needs two cross-lane exchanges per block.
-//   * Long contexts split into partitions of `part_tokens`; partials
-//     (m, l, unnormalised acc) go to the workspace and a second kernel
-//     merges them.  A sequence that fits one partition is written directly.
+// A second kernel merges the partials of the sequences that span waves and writes
+// zeros for sequences with nothing to attend.
 #include <stdlib.h>
 
 #include "ndl_common.hpp"
 
 namespace ndl {
 
-constexpr int kDecodeMinAutoPartition = 64;
-constexpr int kDecodeMaxPartition = 1024;  // 64 blocks: one table entry per lane
+// The fewest tiles a wave of the automatic split takes.
+constexpr int kDecodeMinChunk = 2;
 
 template <int D> struct VRow;
 template <> struct VRow<128> { using T = u32x4; };  // 8 bf16 per lane per token
@@ -56,16 +66,74 @@ struct DecodeArgs {
   int num_heads;
   int group;
   float scale_log2;
-  int part_tokens;
-  int max_parts;
-  float* ws_ml;   // [seq][head][part][2] = (m, l)
-  float* ws_acc;  // [seq][head][part][D]
+  int num_seqs;
+  int chunk;      // C: tiles per wave; 0: ceil(T / waves) from the stream length T
+  int waves;      // waves per kv head
+  int nseg;       // segment slots per kv head: waves per kv head + num_seqs
+  float* ws_ml;   // [kv head][segment][group head][2] = (m, l)
+  float* ws_acc;  // [kv head][segment][group head][D]
 };
 
 __device__ __forceinline__ int64_t attended_len(const DecodeArgs& a, int seq) {
   int64_t L = (int64_t)a.context_lens[seq] + 1;  // attention.py:299
   const int64_t cap = (int64_t)a.max_blocks * 16;  // a table row holds at most W blocks
   return L < cap ? L : cap;
+}
+
+__device__ __forceinline__ int seq_tiles(const DecodeArgs& a, int q) {
+  const int64_t L = attended_len(a, q);
+  return L <= 0 ? 0 : (int)((L + 15) >> 4);
+}
+
+// Inclusive prefix sum over the 64 lanes of a wave.
+__device__ __forceinline__ int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+// Stream position of sequence `target`'s first tile, or of the first sequence that
+// owns tile `tile` (target < 0).  Sequences are scanned 64 at a time; the scan stops at
+// the chunk that holds the answer.  Returns the sequence in *seq (num_seqs if none) and
+// its first tile in *first.
+__device__ __forceinline__ void stream_locate(const DecodeArgs& a, int lane, int target,
+                                              int64_t tile, int* seq, int64_t* first) {
+  int64_t carry = 0;
+  for (int base = 0; base < a.num_seqs; base += 64) {
+    const int q = base + lane;
+    const int n = q < a.num_seqs ? seq_tiles(a, q) : 0;
+    const int incl = wave_incl_scan(n, lane);
+    const int64_t excl = carry + incl - n;
+    const uint64_t hit = target >= 0
+        ? __builtin_amdgcn_ballot_w64(q == target)
+        : __builtin_amdgcn_ballot_w64(q < a.num_seqs && n > 0 && excl + n > tile);
+    if (hit) {
+      const int l = __builtin_ctzll(hit);
+      *seq = base + l;
+      *first = __builtin_amdgcn_readlane((int)(excl - carry), l) + carry;
+      return;
+    }
+    carry += __builtin_amdgcn_readlane(incl, 63);
+  }
+  *seq = a.num_seqs;
+  *first = carry;
+}
+
+// Tiles per wave: the fixed chunk, or the stream length (tiles of all sequences of one
+// kv head) over the waves of a kv head, at least kDecodeMinChunk.
+__device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
+  if (a.chunk > 0) return a.chunk;
+  int64_t total = 0;
+  for (int base = 0; base < a.num_seqs; base += 64) {
+    const int q = base + lane;
+    const int n = q < a.num_seqs ? seq_tiles(a, q) : 0;
+    total += __builtin_amdgcn_readlane(wave_incl_scan(n, lane), 63);
+  }
+  const int64_t c = (total + a.waves - 1) / a.waves;
+  return c < kDecodeMinChunk ? kDecodeMinChunk : c;
 }
 
 template <int D, int NBUF>
@@ -75,43 +143,14 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   using VT = typename VRow<D>::T;
 
   // kv head is the fastest grid index: the 8 head slices of one block (adjacent in
-  // memory) are fetched by workgroups dispatched together.
-  const int kvh = blockIdx.x, part = blockIdx.y, seq = blockIdx.z;
+  // memory) are fetched by waves dispatched together.
+  const int kvh = (int)(blockIdx.x % (unsigned)a.num_kv_heads);
+  const int sw = (int)(blockIdx.x / (unsigned)a.num_kv_heads);   // stream wave of the kv head
   const int lane = threadIdx.x, j = lane >> 4, c = lane & 15;
-  const int64_t L = attended_len(a, seq);
-  const int nparts = L <= 0 ? 1 : (int)((L + a.part_tokens - 1) / a.part_tokens);
-  if (part >= nparts) return;
   const bool head_ok = c < a.group;
   const int head = kvh * a.group + c;
-  u16* const out_row = a.out + ((int64_t)seq * a.num_heads + head) * D + DPL * 4 * j;
-
-  if (L <= 0) {  // nothing to attend: zeros (attention.py:307-308 on an empty context)
-    if (head_ok) {
-#pragma unroll
-      for (int i = 0; i < 4 * DPL / 2; ++i) reinterpret_cast<uint32_t*>(out_row)[i] = 0u;
-    }
-    return;
-  }
-
-  const int t0 = part * a.part_tokens;
-  const int t1 = (int)(t0 + a.part_tokens < L ? t0 + a.part_tokens : L);
-  const int tile0 = t0 >> 4;
-  const int ntiles = (t1 - t0 + 15) >> 4;
-
-  // B operand of S^T = K Q^T: lane (j, c) supplies Q[head c][32 s + 8 j .. +8).
-  bf16x8 qb[KS];
-  {
-    const u16* qrow = a.q + (int64_t)seq * a.q_tok_stride + (int64_t)head * D + 8 * j;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      u32x4 w = head_ok ? ld16(qrow + 32 * s) : u32x4{0u, 0u, 0u, 0u};
-      qb[s] = __builtin_bit_cast(bf16x8, w);
-    }
-  }
-
-  // Block ids of this partition, one per lane (ntiles <= 64).
-  int bt_lane = 0;
-  if (lane < ntiles) bt_lane = a.block_table[(int64_t)seq * a.bt_row_stride + tile0 + lane];
+  const int64_t chunk = stream_chunk(a, lane);
+  const int64_t start = (int64_t)sw * chunk, end = start + chunk;
 
   const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
   const int64_t head_off = (int64_t)kvh * 16 * D;
@@ -127,11 +166,6 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   // row-layout writes and the A-operand reads.
   auto swz = [](int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); };
 
-  f32x4 acc[DPL];
-#pragma unroll
-  for (int b = 0; b < DPL; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = kNegInf, lsum = 0.f;
-
   // One cache block (16 tokens) of K and V in registers.
   struct Tile {
     u32x4 k[KS];
@@ -139,132 +173,185 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     bool bad;
   };
 
-  auto load_tile = [&](int it, Tile& t) {
-    int64_t blk = __builtin_amdgcn_readlane(bt_lane, it);
-    t.bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
-    if (t.bad) blk = 0;
-    const u16* kb = a.kplane + blk * blk_stride + head_off;
-    const u16* vb = a.vplane + blk * blk_stride + head_off;
-#pragma unroll
-    for (int s = 0; s < KS; ++s) t.k[s] = ldg16(kb + k_off + RPI * D * s);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) t.v[i] = load_vrow<D>(vb + v_off + i * D);
-  };
+  // Tiles lt0 .. lt1 of sequence seq (n_tiles in all) for the g heads of kv head kvh,
+  // as segment segid of this kv head.
+  auto segment = [&](const int seq, const int lt0, const int lt1, const int n_tiles,
+                     const int segid) {
+    const int64_t L = attended_len(a, seq);
+    const int t1 = (int)(lt1 * 16 < L ? lt1 * 16 : L);   // one past the last token attended
 
-  auto compute_tile = [&](int it, Tile& t) {
-    __builtin_amdgcn_wave_barrier();  // previous block's LDS reads are issued first
+    // B operand of S^T = K Q^T: lane (j, c) supplies Q[head c][32 s + 8 j .. +8).
+    bf16x8 qb[KS];
+    {
+      const u16* qrow = a.q + (int64_t)seq * a.q_tok_stride + (int64_t)head * D + 8 * j;
 #pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const int r = RPI * s + k_row;
-      *reinterpret_cast<u32x4*>(ktile + r * D + 8 * (k_chunk ^ swz(r))) = t.k[s];
+      for (int s = 0; s < KS; ++s) {
+        u32x4 w = head_ok ? ld16(qrow + 32 * s) : u32x4{0u, 0u, 0u, 0u};
+        qb[s] = __builtin_bit_cast(bf16x8, w);
+      }
     }
-    __builtin_amdgcn_wave_barrier();  // one wave: LDS executes its writes before its reads
-    f32x4 st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      const u32x4 ka = *reinterpret_cast<const u32x4*>(ktile + c * D + 8 * ((j + 4 * s) ^ swz(c)));
-      st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka), qb[s], st,
-                                                   0, 0, 0);
-    }
-    // st[i] is the score of token (tile0+it)*16 + 4j + i for head c.
-    const int pos0 = (tile0 + it) * 16 + 4 * j;
-    const bool partial = t.bad || ((tile0 + it) * 16 + 16 > t1);  // wave-uniform
-    float sc[4];
-    float mt = kNegInf;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const bool ok = !partial || (!t.bad && pos0 + i < t1);
-      sc[i] = ok ? st[i] * a.scale_log2 : kNegInf;
-      mt = fmaxf(mt, sc[i]);
-    }
-    mt = fmaxf(mt, xor_shfl(mt, 16));
-    mt = fmaxf(mt, xor_shfl(mt, 32));
-    const float m_new = fmaxf(m, mt);
-    const float m_use = m_new == kNegInf ? 0.f : m_new;
-    const float alpha = fast_exp2(m - m_use);
-    float p[4];
-    float ps = 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      p[i] = fast_exp2(sc[i] - m_use);
-      ps += p[i];
-    }
-    lsum = lsum * alpha + ps;
-    m = m_new;
-    if (__ballot(alpha != 1.f)) {  // rescale only when some head's max moved
-#pragma unroll
-      for (int b = 0; b < DPL; ++b) acc[b] *= alpha;
-    }
+    const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
 
-    if (partial) {  // masked rows may hold stale bits (NaN * 0 = NaN): clear them
+    f32x4 acc[DPL];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const bool ok = !t.bad && pos0 + i < t1;
-        if (!ok) t.v[i] = VT{};
+    for (int b = 0; b < DPL; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float m = kNegInf, lsum = 0.f;
+
+    // Tiles go in windows of 64 (block ids of a window held one per lane).
+    for (int w0 = lt0; w0 < lt1; w0 += 64) {
+      const int ntiles = lt1 - w0 < 64 ? lt1 - w0 : 64;
+      const int bt_lane = lane < ntiles ? bt_row[w0 + lane] : 0;
+
+      auto load_tile = [&](int it, Tile& t) {
+        int64_t blk = __builtin_amdgcn_readlane(bt_lane, it);
+        t.bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
+        if (t.bad) blk = 0;
+        const u16* kb = a.kplane + blk * blk_stride + head_off;
+        const u16* vb = a.vplane + blk * blk_stride + head_off;
+#pragma unroll
+        for (int s = 0; s < KS; ++s) t.k[s] = ldg16(kb + k_off + RPI * D * s);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) t.v[i] = load_vrow<D>(vb + v_off + i * D);
+      };
+
+      auto compute_tile = [&](int it, Tile& t) {
+        __builtin_amdgcn_wave_barrier();  // previous block's LDS reads are issued first
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const int r = RPI * s + k_row;
+          *reinterpret_cast<u32x4*>(ktile + r * D + 8 * (k_chunk ^ swz(r))) = t.k[s];
+        }
+        __builtin_amdgcn_wave_barrier();  // one wave: LDS executes its writes before its reads
+        f32x4 st = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const u32x4 ka =
+              *reinterpret_cast<const u32x4*>(ktile + c * D + 8 * ((j + 4 * s) ^ swz(c)));
+          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka), qb[s], st,
+                                                       0, 0, 0);
+        }
+        // st[i] is the score of token (w0+it)*16 + 4j + i for head c.
+        const int pos0 = (w0 + it) * 16 + 4 * j;
+        const bool partial = t.bad || ((w0 + it) * 16 + 16 > t1);  // wave-uniform
+        float sc[4];
+        float mt = kNegInf;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const bool ok = !partial || (!t.bad && pos0 + i < t1);
+          sc[i] = ok ? st[i] * a.scale_log2 : kNegInf;
+          mt = fmaxf(mt, sc[i]);
+        }
+        mt = fmaxf(mt, xor_shfl(mt, 16));
+        mt = fmaxf(mt, xor_shfl(mt, 32));
+        const float m_new = fmaxf(m, mt);
+        const float m_use = m_new == kNegInf ? 0.f : m_new;
+        const float alpha = fast_exp2(m - m_use);
+        float p[4];
+        float ps = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = fast_exp2(sc[i] - m_use);
+          ps += p[i];
+        }
+        lsum = lsum * alpha + ps;
+        m = m_new;
+        if (__ballot(alpha != 1.f)) {  // rescale only when some head's max moved
+#pragma unroll
+          for (int b = 0; b < DPL; ++b) acc[b] *= alpha;
+        }
+
+        if (partial) {  // masked rows may hold stale bits (NaN * 0 = NaN): clear them
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool ok = !t.bad && pos0 + i < t1;
+            if (!ok) t.v[i] = VT{};
+          }
+        }
+
+        const i16x4 pb = __builtin_bit_cast(
+            i16x4, u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])});
+#pragma unroll
+        for (int b = 0; b < DPL; ++b) {
+          const uint32_t w01 = pack_halves(t.v[0][b >> 1], t.v[1][b >> 1], b & 1);
+          const uint32_t w23 = pack_halves(t.v[2][b >> 1], t.v[3][b >> 1], b & 1);
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
+              __builtin_bit_cast(i16x4, u32x2{w01, w23}), pb, acc[b], 0, 0, 0);
+        }
+      };
+
+      // NBUF-deep ring: while block `it` computes, blocks it+1 .. it+NBUF-1 are in flight.
+      Tile buf[NBUF];
+#pragma unroll
+      for (int u = 0; u < NBUF - 1; ++u)
+        if (u < ntiles) load_tile(u, buf[u]);
+      for (int it = 0; it < ntiles; it += NBUF) {
+#pragma unroll
+        for (int u = 0; u < NBUF; ++u) {
+          const int nxt = it + u + NBUF - 1;
+          if (nxt < ntiles) load_tile(nxt, buf[(u + NBUF - 1) % NBUF]);
+          if (it + u < ntiles) compute_tile(it + u, buf[u]);
+        }
       }
     }
 
-    const i16x4 pb = __builtin_bit_cast(
-        i16x4, u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])});
+    lsum += xor_shfl(lsum, 16);
+    lsum += xor_shfl(lsum, 32);
+    if (!head_ok) return;
+
+    // acc[b][i] holds O[head c][d = DPL * (4 j + i) + b].
+    if (lt0 == 0 && lt1 == n_tiles) {  // the whole sequence: final output
+      u16* const out_row = a.out + ((int64_t)seq * a.num_heads + head) * D + DPL * 4 * j;
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
-    for (int b = 0; b < DPL; ++b) {
-      const uint32_t w01 = pack_halves(t.v[0][b >> 1], t.v[1][b >> 1], b & 1);
-      const uint32_t w23 = pack_halves(t.v[2][b >> 1], t.v[3][b >> 1], b & 1);
-      acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-          __builtin_bit_cast(i16x4, u32x2{w01, w23}), pb, acc[b], 0, 0, 0);
+      for (int i = 0; i < 4; ++i) {
+        uint32_t w[DPL / 2];
+#pragma unroll
+        for (int b = 0; b < DPL; b += 2)
+          w[b / 2] = pack_bf16x2(acc[b][i] * inv, acc[b + 1][i] * inv);
+        if constexpr (DPL == 8)
+          st16(out_row + DPL * i, u32x4{w[0], w[1], w[2], w[3]});
+        else
+          *reinterpret_cast<u32x2*>(out_row + DPL * i) = u32x2{w[0], w[1]};
+      }
+    } else {
+      const int64_t slot = ((int64_t)kvh * a.nseg + segid) * a.group + c;
+      float* dst = a.ws_acc + slot * D + DPL * 4 * j;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+#pragma unroll
+        for (int b = 0; b < DPL; b += 4)
+          *reinterpret_cast<f32x4*>(dst + DPL * i + b) =
+              f32x4{acc[b][i], acc[b + 1][i], acc[b + 2][i], acc[b + 3][i]};
+      }
+      if (j == 0) {
+        a.ws_ml[slot * 2] = m;
+        a.ws_ml[slot * 2 + 1] = lsum;
+      }
     }
   };
 
-  // NBUF-deep ring: while block `it` computes, blocks it+1 .. it+NBUF-1 are in flight.
-  Tile buf[NBUF];
-#pragma unroll
-  for (int u = 0; u < NBUF - 1; ++u)
-    if (u < ntiles) load_tile(u, buf[u]);
-  for (int it = 0; it < ntiles; it += NBUF) {
-#pragma unroll
-    for (int u = 0; u < NBUF; ++u) {
-      const int nxt = it + u + NBUF - 1;
-      if (nxt < ntiles) load_tile(nxt, buf[(u + NBUF - 1) % NBUF]);
-      if (it + u < ntiles) compute_tile(it + u, buf[u]);
+  // Walk the sequences that own tiles start .. end of this kv head's stream.
+  int seq;
+  int64_t first;
+  stream_locate(a, lane, -1, start, &seq, &first);
+  while (seq < a.num_seqs && first < end) {
+    const int nt = seq_tiles(a, seq);
+    if (nt > 0) {
+      const int64_t s0 = start > first ? start : first;
+      const int64_t s1 = end < first + nt ? end : first + nt;
+      segment(seq, (int)(s0 - first), (int)(s1 - first), nt, sw + seq);
     }
-  }
-
-  lsum += xor_shfl(lsum, 16);
-  lsum += xor_shfl(lsum, 32);
-  if (!head_ok) return;
-
-  // acc[b][i] holds O[head c][d = DPL * (4 j + i) + b].
-  if (nparts == 1) {
-    const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t w[DPL / 2];
-#pragma unroll
-      for (int b = 0; b < DPL; b += 2) w[b / 2] = pack_bf16x2(acc[b][i] * inv, acc[b + 1][i] * inv);
-      if constexpr (DPL == 8)
-        st16(out_row + DPL * i, u32x4{w[0], w[1], w[2], w[3]});
-      else
-        *reinterpret_cast<u32x2*>(out_row + DPL * i) = u32x2{w[0], w[1]};
-    }
-  } else {
-    const int64_t slot = ((int64_t)seq * a.num_heads + head) * a.max_parts + part;
-    float* dst = a.ws_acc + slot * D + DPL * 4 * j;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-#pragma unroll
-      for (int b = 0; b < DPL; b += 4)
-        *reinterpret_cast<f32x4*>(dst + DPL * i + b) =
-            f32x4{acc[b][i], acc[b + 1][i], acc[b + 2][i], acc[b + 3][i]};
-    }
-    if (j == 0) {
-      a.ws_ml[slot * 2] = m;
-      a.ws_ml[slot * 2 + 1] = lsum;
-    }
+    first += nt;
+    ++seq;
   }
 }
 
-// Merge of the partition partials: one wave per (query head, sequence).
-// Pass 1 (lane-parallel over partitions): global max, weights w_p = 2^(m_p - M)
+// Merge of the segment partials: one wave per (query head, sequence).  A sequence
+// whose tiles lie in waves s0 .. s1 of its kv head's stream has its partials in
+// segment slots s0 + seq .. s1 + seq; a sequence inside one wave was written by the
+// attention kernel, and one with nothing to attend gets zeros here
+// (attention.py:307-308 on an empty context).
+// Pass 1 (lane-parallel over segments): global max, weights w_p = 2^(m_p - M)
 // into LDS, denominator sum_p w_p l_p.  Pass 2: sum_p w_p acc_p; the first
 // kMergePrefetch partials were loaded together with the (m, l) pairs, the rest
 // with independent, unrolled loads.
@@ -276,30 +363,45 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int PER_LANE = D / 64;
   __shared__ float wsh[kMergeMaxParts];
   const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
-  const int64_t L = attended_len(a, seq);
-  const int nparts = L <= 0 ? 1 : (int)((L + a.part_tokens - 1) / a.part_tokens);
-  if (nparts <= 1) return;
-  const int64_t base = ((int64_t)seq * a.num_heads + head) * a.max_parts;
-  const float* __restrict__ ml = a.ws_ml + base * 2;
-  const float* __restrict__ src = a.ws_acc + base * D + lane * PER_LANE;
+  const int kvh = head / a.group, hc = head - kvh * a.group;
+  u16* dst = a.out + ((int64_t)seq * a.num_heads + head) * D + lane * PER_LANE;
+  const int nt = seq_tiles(a, seq);
+  if (nt == 0) {
+    if constexpr (PER_LANE == 2)
+      *reinterpret_cast<uint32_t*>(dst) = 0u;
+    else
+      dst[0] = 0;
+    return;
+  }
+  int found;
+  int64_t first;
+  stream_locate(a, lane, seq, 0, &found, &first);
+  const int64_t chunk = stream_chunk(a, lane);
+  const int64_t s0 = first / chunk, s1 = (first + nt - 1) / chunk;
+  if (s0 == s1) return;
+  const int nparts = (int)(s1 - s0 + 1);
+  const int64_t slot0 = ((int64_t)kvh * a.nseg + s0 + seq) * a.group + hc;
+  const int64_t ml_stride = 2 * (int64_t)a.group, acc_stride = (int64_t)a.group * D;
+  const float* __restrict__ ml = a.ws_ml + slot0 * 2;
+  const float* __restrict__ src = a.ws_acc + slot0 * D + lane * PER_LANE;
 
   // The first partials do not depend on the weights: load them with the (m, l) pairs.
   float pre[kMergePrefetch][PER_LANE];
 #pragma unroll
   for (int u = 0; u < kMergePrefetch; ++u)
 #pragma unroll
-    for (int e = 0; e < PER_LANE; ++e) pre[u][e] = u < nparts ? src[(int64_t)u * D + e] : 0.f;
+    for (int e = 0; e < PER_LANE; ++e) pre[u][e] = u < nparts ? src[u * acc_stride + e] : 0.f;
 
   float mx = kNegInf;
-  for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, ml[2 * p]);
+  for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, ml[p * ml_stride]);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, xor_shfl(mx, o));
   float den = 0.f;
   for (int p = lane; p < nparts; p += 64) {
-    const float mp = ml[2 * p];
+    const float mp = ml[p * ml_stride];
     const float w = (mp == kNegInf || mx == kNegInf) ? 0.f : fast_exp2(mp - mx);
     wsh[p] = w;
-    den += w * ml[2 * p + 1];
+    den += w * ml[p * ml_stride + 1];
   }
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) den += xor_shfl(den, o);
@@ -319,7 +421,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
-      for (int e = 0; e < PER_LANE; ++e) v[u][e] = src[(int64_t)(p + u) * D + e];
+      for (int e = 0; e < PER_LANE; ++e) v[u][e] = src[(p + u) * acc_stride + e];
 #pragma unroll
     for (int u = 0; u < 4; ++u)
 #pragma unroll
@@ -327,10 +429,9 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   }
   for (; p < nparts; ++p)
 #pragma unroll
-    for (int e = 0; e < PER_LANE; ++e) acc[e] += wsh[p] * src[(int64_t)p * D + e];
+    for (int e = 0; e < PER_LANE; ++e) acc[e] += wsh[p] * src[p * acc_stride + e];
 
   const float inv = den > 0.f ? 1.f / den : 0.f;
-  u16* dst = a.out + ((int64_t)seq * a.num_heads + head) * D + lane * PER_LANE;
   if constexpr (PER_LANE == 2)
     *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc[0] * inv, acc[1] * inv);
   else
@@ -347,42 +448,82 @@ inline int decode_pipeline_depth() {
   return depth;
 }
 
-// Partition size.  The default aims at ~16k waves' worth of (sequence, head, partition)
-// slots: W*16*B*H / 16384 tokens, rounded up to a power of two in [64, 1024].  Small
-// batches get short partitions (enough waves to cover the GPU); large ones get long
-// partitions (few partials to merge).
-inline int decode_partition(int partition_tokens, int num_seqs, int num_heads, int max_blocks) {
+// Resident waves of the attention kernel on the current device (CUs times waves per CU),
+// cached per device and kernel; 0 when the device cannot be queried.
+inline int64_t decode_resident_waves(const void* fn) {
+  struct Entry { const void* fn; int dev; int64_t waves; };
+  static Entry cache[32];
+  static int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  for (int i = 0; i < used; ++i)
+    if (cache[i].fn == fn && cache[i].dev == dev) return cache[i].waves;
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64, 0) != hipSuccess ||
+      cus <= 0 || per_cu <= 0)
+    return 0;
+  const int64_t waves = (int64_t)cus * per_cu;
+  if (used < 32) cache[used++] = Entry{fn, dev, waves};
+  return waves;
+}
+
+template <int D> const void* decode_kernel_fn(int depth) {
+  return depth == 2 ? (const void*)paged_decode_kernel<D, 2>
+                    : depth == 4 ? (const void*)paged_decode_kernel<D, 4>
+                                 : (const void*)paged_decode_kernel<D, 3>;
+}
+
+struct DecodeLayout {
+  int64_t chunk;        // fixed tiles per wave, or 0 (from the stream length on the device)
+  int64_t waves;        // waves per kv head
+  int64_t nseg;         // segment slots per kv head
+  size_t ml_bytes;      // (m, l) region, 256-byte aligned
+  size_t bytes;         // whole workspace
+};
+
+// Split of the stream.  partition_tokens > 0 (a multiple of 16) fixes the tokens per
+// wave.  Otherwise the launch holds as many waves as can be resident at once, shared
+// by the kv heads, so that every wave that has tiles runs from the start (a device
+// that cannot be queried gets 2048); each takes ceil(T / waves) tiles of its stream.
+inline int decode_layout(int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                         int max_blocks, int partition_tokens, DecodeLayout* lay) {
   if (partition_tokens > 0) {
-    if (partition_tokens % 16 != 0 || partition_tokens > kDecodeMaxPartition) return -1;
-    return partition_tokens;
+    if (partition_tokens % 16 != 0) return NDL_ERR_INVALID_ARG;
+    lay->chunk = partition_tokens / 16;
+    lay->waves = ((int64_t)num_seqs * max_blocks + lay->chunk - 1) / lay->chunk;
+  } else {
+    int64_t resident = decode_resident_waves(
+        head_dim == 128 ? decode_kernel_fn<128>(decode_pipeline_depth())
+                        : decode_kernel_fn<64>(decode_pipeline_depth()));
+    if (resident <= 0) resident = 2048;
+    int64_t w = resident / num_kv_heads;
+    if (w < 1) w = 1;
+    if (w > kMergeMaxParts - 2) w = kMergeMaxParts - 2;  // segments of one sequence
+    lay->chunk = 0;
+    lay->waves = w;
   }
-  const double work = (double)max_blocks * 16.0 * num_seqs * num_heads / 16384.0;
-  int p = kDecodeMinAutoPartition;
-  while (p < kDecodeMaxPartition && p < work) p <<= 1;
-  return p;
+  lay->nseg = lay->waves + num_seqs;
+  const size_t slots = (size_t)num_kv_heads * lay->nseg * (num_heads / num_kv_heads);
+  lay->ml_bytes = (slots * 2 * sizeof(float) + 255) & ~(size_t)255;
+  lay->bytes = lay->ml_bytes + slots * head_dim * sizeof(float);
+  return NDL_OK;
 }
-
-inline int64_t decode_max_parts(int max_blocks, int part) {
-  return ((int64_t)max_blocks * 16 + part - 1) / part;
-}
-
-inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 }  // namespace ndl
 
-extern "C" size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int head_dim,
-                                                   int max_blocks_per_seq, int block_size,
-                                                   int partition_tokens) {
+extern "C" size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
+                                                   int head_dim, int max_blocks_per_seq,
+                                                   int block_size, int partition_tokens) {
   using namespace ndl;
-  if (num_seqs <= 0 || num_heads <= 0 || head_dim <= 0 || max_blocks_per_seq <= 0 ||
-      block_size != 16)
+  if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
+      head_dim <= 0 || max_blocks_per_seq <= 0 || block_size != 16)
     return 0;
-  const int part = decode_partition(partition_tokens, num_seqs, num_heads, max_blocks_per_seq);
-  if (part < 0) return 0;
-  const int64_t parts = decode_max_parts(max_blocks_per_seq, part);
-  if (parts <= 1) return 0;
-  const size_t slots = (size_t)num_seqs * num_heads * parts;
-  return align256(slots * 2 * sizeof(float)) + slots * head_dim * sizeof(float);
+  DecodeLayout lay;
+  if (decode_layout(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                    partition_tokens, &lay) != NDL_OK)
+    return 0;
+  return lay.bytes;
 }
 
 extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
@@ -406,16 +547,18 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
   if (!out || !q || !kv_cache || !block_table || !context_lens) return NDL_ERR_INVALID_ARG;
   if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)kv_cache) & 15u) return NDL_ERR_INVALID_ARG;
   if (q_tok_stride & 7) return NDL_ERR_INVALID_ARG;
-  if (num_seqs > 65535 || num_kv_heads > 65535) return NDL_ERR_UNSUPPORTED;
-  const int part = decode_partition(partition_tokens, num_seqs, num_heads, max_blocks_per_seq);
-  if (part < 0) return NDL_ERR_INVALID_ARG;
-
-  const int64_t max_parts = decode_max_parts(max_blocks_per_seq, part);
-  if (max_parts > kMergeMaxParts) return NDL_ERR_UNSUPPORTED;
-  const size_t need = ndl_paged_decode_workspace_bytes(num_seqs, num_heads, head_dim,
-                                                       max_blocks_per_seq, block_size, part);
-  if (max_parts > 1 && (workspace == nullptr || workspace_bytes < need ||
-                        ((uintptr_t)workspace & 15u)))
+  if (num_seqs > 65535) return NDL_ERR_UNSUPPORTED;
+  DecodeLayout lay;
+  const int rc0 = decode_layout(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+                                partition_tokens, &lay);
+  if (rc0 != NDL_OK) return rc0;
+  // Segments one sequence can span: its tiles over the chunk, plus the partial ends
+  // (the automatic split keeps waves <= kMergeMaxParts - 2).
+  if (lay.chunk > 0 && (int64_t)max_blocks_per_seq / lay.chunk + 2 > kMergeMaxParts)
+    return NDL_ERR_UNSUPPORTED;
+  const int64_t grid_waves = lay.waves * num_kv_heads;
+  if (grid_waves > 0x7fffffff || lay.nseg > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
+  if (workspace == nullptr || workspace_bytes < lay.bytes || ((uintptr_t)workspace & 15u))
     return NDL_ERR_WORKSPACE;
 
   DecodeArgs a;
@@ -433,15 +576,15 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
   a.num_heads = num_heads;
   a.group = group;
   a.scale_log2 = scale * kLog2e;
-  a.part_tokens = part;
-  a.max_parts = (int)max_parts;
-  const size_t slots = (size_t)num_seqs * num_heads * max_parts;
+  a.num_seqs = num_seqs;
+  a.chunk = (int)lay.chunk;
+  a.waves = (int)lay.waves;
+  a.nseg = (int)lay.nseg;
   a.ws_ml = (float*)workspace;
-  a.ws_acc = max_parts > 1 ? (float*)((char*)workspace + align256(slots * 2 * sizeof(float)))
-                           : nullptr;
+  a.ws_acc = (float*)((char*)workspace + lay.ml_bytes);
 
   hipStream_t s = (hipStream_t)stream;
-  const dim3 grid((unsigned)num_kv_heads, (unsigned)max_parts, (unsigned)num_seqs);
+  const dim3 grid((unsigned)grid_waves);
   const int depth = decode_pipeline_depth();
   if (head_dim == 128) {
     if (depth == 2)
@@ -459,7 +602,7 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
       hipLaunchKernelGGL((paged_decode_kernel<64, 3>), grid, dim3(64), 0, s, a);
   }
   int rc = check_launch();
-  if (rc != NDL_OK || max_parts <= 1) return rc;
+  if (rc != NDL_OK) return rc;
   const dim3 mgrid((unsigned)num_heads, (unsigned)num_seqs);
   if (head_dim == 128)
     hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, s, a);

@@ -111,8 +111,8 @@ class Attention(nn.Module):
         return self._decode_attend(q, kv_cache, block_table, context_lens)
 
     def _decode_attend(self, q, kv_cache, block_table, context_lens):
-        need = ops.decode_workspace_bytes(q.shape[0], self.num_heads, self.head_dim,
-                                          block_table.shape[1], kv_cache.shape[3])
+        need = ops.decode_workspace_bytes(q.shape[0], self.num_heads, self.num_kv_heads,
+                                          self.head_dim, block_table.shape[1], kv_cache.shape[3])
         ws = self._workspace
         if need and (ws is None or ws.numel() < need or ws.device != q.device):
             ws = self._workspace = torch.empty(need, dtype=torch.uint8, device=q.device)

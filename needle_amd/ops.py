@@ -182,11 +182,12 @@ def write_kv(k, v, kv_cache, block_table, cu_seqlens, context_lens) -> None:
     kv_append(k, v, kv_cache, block_table, context_lens, cu_seqlens=cu_seqlens)
 
 
-def decode_workspace_bytes(num_seqs: int, num_heads: int, head_dim: int,
+def decode_workspace_bytes(num_seqs: int, num_heads: int, num_kv_heads: int, head_dim: int,
                            max_blocks_per_seq: int, block_size: int = 16,
                            partition_tokens: int = 0) -> int:
     return int(_lib.load().ndl_paged_decode_workspace_bytes(
-        num_seqs, num_heads, head_dim, max_blocks_per_seq, block_size, partition_tokens))
+        num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq, block_size,
+        partition_tokens))
 
 
 def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
@@ -223,7 +224,7 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
     lib = _lib.load()
     w = block_table.shape[1]
     need = int(lib.ndl_paged_decode_workspace_bytes(
-        n_seqs, num_heads, head_dim, w, bs, partition_tokens))
+        n_seqs, num_heads, num_kv_heads, head_dim, w, bs, partition_tokens))
     if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None

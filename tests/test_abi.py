@@ -45,16 +45,23 @@ def test_version_and_status_text(lib):
 
 
 def test_decode_workspace_sizing(lib):
-    # 2 sequences x 32 heads, W = 64 blocks = 1024 tokens, partitions of 256 -> 4 parts
-    n = lib.ndl_paged_decode_workspace_bytes(2, 32, 128, 64, 16, 256)
-    slots = 2 * 32 * 4
+    # 2 sequences x 32 heads over 8 kv heads, W = 64 blocks, 256 tokens (16 tiles) per
+    # wave -> ceil(2 * 64 / 16) = 8 waves per kv head, 8 + 2 segment slots per kv head,
+    # one (m, l) pair and one head_dim row per (kv head, segment, group head).
+    n = lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 256)
+    slots = 8 * (8 + 2) * 4
     ml = (slots * 2 * 4 + 255) // 256 * 256
     assert n == ml + slots * 128 * 4
-    # a single partition needs no scratch
-    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 128, 16, 16, 256) == 0
-    # unsupported block size / bad partition
-    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 128, 64, 32, 256) == 0
-    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 128, 64, 16, 100) == 0
+    # automatic split: the resident waves of the device (2048 when there is none to
+    # ask) shared by the 8 kv heads; same slot formula
+    n = lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 0)
+    fits = [w for w in range(1, 4096)
+            if n == (8 * (w + 2) * 4 * 8 + 255) // 256 * 256 + 8 * (w + 2) * 4 * 128 * 4]
+    assert len(fits) == 1
+    # unsupported block size / partition not a multiple of 16 / heads not a multiple
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 32, 256) == 0
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 100) == 0
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 6, 128, 64, 16, 0) == 0
 
 
 def test_rejections_before_any_launch(lib):

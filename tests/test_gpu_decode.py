@@ -119,3 +119,55 @@ def test_repeat_calls_are_deterministic():
     b = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
                          s.num_heads, s.num_kv_heads, s.head_dim).float().cpu()
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("part", [0, 16])
+def test_empty_contexts_give_zeros_between_live_ones(part):
+    # context_lens + 1 <= 0: nothing to attend (the reference's empty softmax gives zeros);
+    # the neighbours' tiles share the waves those sequences would sit between
+    case = wl.decode_case(wl.LLAMA3_8B, [40, 3, 700, 0, 90], seed=206, garbage=False)
+    case.context_lens = torch.tensor([40, -1, 700, -5, 90], dtype=torch.int32)
+    case.ctx = [40, -1, 700, -5, 90]
+    s = case.shape
+    g = case.to(DEV)
+    out = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
+                           s.num_heads, s.num_kv_heads, s.head_dim, partition_tokens=part)
+    torch.cuda.synchronize()
+    got = out.float().cpu()
+    assert torch.equal(got[1], torch.zeros_like(got[1]))
+    assert torch.equal(got[3], torch.zeros_like(got[3]))
+    live = [0, 2, 4]
+    want = paged_ref.decode_pytorch(case.q[live], case.kv_cache, case.block_table[live],
+                                    case.context_lens[live], s.scale, s.num_heads,
+                                    s.num_kv_heads, s.head_dim)
+    assert_close(got[live], want.float())
+
+
+def test_invalid_block_ids_are_skipped():
+    """A block id outside [0, num_blocks) is never dereferenced: its keys are dropped."""
+    shape = wl.LLAMA3_8B
+    case = wl.decode_case(shape, [100, 300], seed=207, garbage=False)
+    nb = case.kv_cache.shape[1]
+    bt = case.block_table.clone()
+    bt[0, 2] = -4          # tokens 32..47 of sequence 0
+    bt[1, 5] = nb + 3      # tokens 80..95 of sequence 1
+    case.block_table = bt
+    s = case.shape
+    g = case.to(DEV)
+    out = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
+                           s.num_heads, s.num_kv_heads, s.head_dim, partition_tokens=64)
+    torch.cuda.synchronize()
+    kvn = case.kv_cache.double().numpy()
+    qn = case.q.double().numpy()
+    btl = bt.tolist()
+    want = np.zeros(out.shape)
+    for i, ctx in enumerate(case.ctx):
+        keys = [p for p in range(ctx + 1) if 0 <= btl[i][p // 16] < nb]
+        for h in range(s.num_heads):
+            kvh = h // s.group
+            kr = np.stack([kvn[0, btl[i][p // 16], kvh, p % 16] for p in keys])
+            vr = np.stack([kvn[1, btl[i][p // 16], kvh, p % 16] for p in keys])
+            sc = kr @ qn[i, h] * s.scale
+            pr = np.exp(sc - sc.max())
+            want[i, h] = pr @ vr / pr.sum()
+    assert_close(out.float().cpu(), want)
