@@ -54,9 +54,11 @@ def parse_args():
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine run")
     p.add_argument("--e2e-seconds", type=float, default=120.0,
                    help="time limit of the end-to-end run (it finishes in about 30 s)")
-    p.add_argument("--profile", action="store_true",
-                   help="counter-collection driver: --steps steps of the workload, then three "
-                        "1 GiB device copies (the calibration kernel), no timing output")
+    p.add_argument("--profile", nargs="?", const="decode", choices=["decode", "prefill"],
+                   help="counter-collection driver, no timing output: --steps steps of the "
+                        "decode workload (decode) or --steps rounds of the Qwen2-7B varlen "
+                        "append + prefill (prefill), then three 1 GiB device copies (the "
+                        "calibration kernel)")
     return p.parse_args()
 
 
@@ -277,17 +279,33 @@ def main():
             decode_layer(l)
 
     if args.profile:
-        for _ in range(args.steps):
-            step()
+        info = {"profile": args.profile, "profile_steps": args.steps}
+        if args.profile == "decode":
+            for _ in range(args.steps):
+                step()
+            info.update(layers=LAYERS,
+                        decode_algorithmic_bytes_per_launch=wl.decode_bytes(shape, ctx, width))
+        else:
+            del pools
+            torch.cuda.empty_cache()
+            c3 = wl.config_case("qwen2-7b-prefill", device=dev, garbage=False)
+            s3 = c3.shape
+            for _ in range(args.steps):
+                ops.write_kv(c3.k, c3.v, c3.kv_cache, c3.block_table, c3.cu_seqlens,
+                             c3.context_lens)
+                ops.varlen_prefill(c3.q, c3.kv_cache, c3.block_table, c3.cu_seqlens,
+                                   c3.context_lens, c3.max_seqlen, s3.scale, s3.num_heads,
+                                   s3.num_kv_heads, s3.head_dim)
+            info.update(append_algorithmic_bytes=wl.append_bytes(s3, sum(c3.new_lens),
+                                                                   c3.num_seqs, varlen=True),
+                        prefill_algorithmic_flops=wl.prefill_flops(s3, c3.new_lens))
         src = torch.empty(1 << 29, dtype=torch.bfloat16, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
             dst.copy_(src)
         torch.cuda.synchronize()
-        print(json.dumps({"profile_steps": args.steps, "layers": LAYERS,
-                          "decode_algorithmic_bytes_per_launch":
-                              wl.decode_bytes(shape, ctx, width),
-                          "calibration_copy_bytes_read": src.numel() * 2}), flush=True)
+        info["calibration_copy_bytes_read"] = src.numel() * 2
+        print(json.dumps(info), flush=True)
         return
 
     for _ in range(args.warmup):
