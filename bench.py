@@ -263,7 +263,7 @@ def main():
     ws_bytes = ops.decode_workspace_bytes(len(ctx), shape.num_heads, shape.num_kv_heads,
                                           shape.head_dim, width,
                                           shape.block_size, args.partition)
-    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=dev)
+    ws = ops.decode_workspace(ws_bytes, dev)
     h, hkv, d, sc = shape.num_heads, shape.num_kv_heads, shape.head_dim, shape.scale
 
     def decode_layer(l):

@@ -173,6 +173,30 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     bool bad;
   };
 
+  // Partial (fp32 m, l, unnormalised acc) of a piece into segment slot segid.
+  auto store_partial = [&](const int segid, const f32x4 (&o)[DPL], const float mv,
+                           const float lv) {
+    const int64_t slot = ((int64_t)kvh * a.nseg + segid) * a.group + c;
+    float* dst = a.ws_acc + slot * D + DPL * 4 * j;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int b = 0; b < DPL; b += 4)
+        *reinterpret_cast<f32x4*>(dst + DPL * i + b) =
+            f32x4{o[b][i], o[b + 1][i], o[b + 2][i], o[b + 3][i]};
+    }
+    if (j == 0) {
+      a.ws_ml[slot * 2] = mv;
+      a.ws_ml[slot * 2 + 1] = lv;
+    }
+  };
+  // The piece that ends a sequence at the start of this wave's tiles is held in registers
+  // and stored after the walk: stores count in the same in-order counter as loads, so
+  // storing it at once would make the next sequence's first loads wait for the stores.
+  f32x4 held[DPL];
+  float held_m = 0.f, held_l = 0.f;
+  int held_seg = -1;
+
   // Tiles lt0 .. lt1 of sequence seq (n_tiles in all) for the g heads of kv head kvh,
   // as segment segid of this kv head.
   auto segment = [&](const int seq, const int lt0, const int lt1, const int n_tiles,
@@ -313,20 +337,14 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
         else
           *reinterpret_cast<u32x2*>(out_row + DPL * i) = u32x2{w[0], w[1]};
       }
+    } else if (lt0 > 0 && lt1 == n_tiles && held_seg < 0) {
+#pragma unroll
+      for (int b = 0; b < DPL; ++b) held[b] = acc[b];
+      held_m = m;
+      held_l = lsum;
+      held_seg = segid;
     } else {
-      const int64_t slot = ((int64_t)kvh * a.nseg + segid) * a.group + c;
-      float* dst = a.ws_acc + slot * D + DPL * 4 * j;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-#pragma unroll
-        for (int b = 0; b < DPL; b += 4)
-          *reinterpret_cast<f32x4*>(dst + DPL * i + b) =
-              f32x4{acc[b][i], acc[b + 1][i], acc[b + 2][i], acc[b + 3][i]};
-      }
-      if (j == 0) {
-        a.ws_ml[slot * 2] = m;
-        a.ws_ml[slot * 2 + 1] = lsum;
-      }
+      store_partial(segid, acc, m, lsum);
     }
   };
 
@@ -344,6 +362,7 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     first += nt;
     ++seq;
   }
+  if (held_seg >= 0) store_partial(held_seg, held, held_m, held_l);
 }
 
 // Merge of the segment partials: one wave per (query head, sequence).  A sequence

@@ -114,8 +114,8 @@ class Attention(nn.Module):
         need = ops.decode_workspace_bytes(q.shape[0], self.num_heads, self.num_kv_heads,
                                           self.head_dim, block_table.shape[1], kv_cache.shape[3])
         ws = self._workspace
-        if need and (ws is None or ws.numel() < need or ws.device != q.device):
-            ws = self._workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        if ws is None or ws.numel() < need or ws.device != q.device:
+            ws = self._workspace = ops.decode_workspace(need, q.device)
         return ops.paged_decode(q, kv_cache, block_table, context_lens, self.scale,
                                 self.num_heads, self.num_kv_heads, self.head_dim,
-                                workspace=ws if need else None)
+                                workspace=ws)

@@ -225,16 +225,23 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
     w = block_table.shape[1]
     need = int(lib.ndl_paged_decode_workspace_bytes(
         n_seqs, num_heads, num_kv_heads, head_dim, w, bs, partition_tokens))
-    if need and (workspace is None or workspace.numel() * workspace.element_size() < need):
-        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-    ws_ptr = workspace.data_ptr() if (need and workspace is not None) else None
+    _require(need > 0, "unsupported decode shape")
+    if workspace is None or workspace.numel() * workspace.element_size() < need:
+        workspace = decode_workspace(need, dev)
     rc = lib.ndl_paged_decode(
         out.data_ptr(), q.data_ptr(), qs, kv_cache.data_ptr(), num_blocks,
         block_table.data_ptr(), block_table.stride(0), w,
         context_lens.data_ptr(), n_seqs, num_heads, num_kv_heads, head_dim, bs,
-        _DTYPES[q.dtype], float(scale), partition_tokens, ws_ptr, need, _stream(dev))
+        _DTYPES[q.dtype], float(scale), partition_tokens, workspace.data_ptr(), need,
+        _stream(dev))
     _lib.check(rc, "ndl_paged_decode")
     return out
+
+
+def decode_workspace(nbytes: int, device) -> torch.Tensor:
+    """Scratch for ndl_paged_decode (no contents are assumed; calls that share one must
+    run in stream order)."""
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
 
 
 def varlen_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,

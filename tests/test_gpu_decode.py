@@ -171,3 +171,73 @@ def test_invalid_block_ids_are_skipped():
             pr = np.exp(sc - sc.max())
             want[i, h] = pr @ vr / pr.sum()
     assert_close(out.float().cpu(), want)
+
+
+def test_one_workspace_across_calls_and_batch_sizes():
+    """Sequences split over several waves leave partials in the workspace for the merge.
+    One workspace serves a small batch, then a larger one, then both again, and a foreign
+    workspace full of other bytes: every output equals that of a call with a fresh
+    workspace."""
+    s = wl.LLAMA3_8B
+    small = wl.decode_case(s, [5000, 7000, 3000], seed=208).to(DEV)
+    large = wl.decode_case(s, [300, 4100, 17, 2500, 9000, 64, 1200, 6000, 0, 800], seed=209)
+    want_large, _ = run_oracle(large)
+    large = large.to(DEV)
+    for c in (small, large):
+        ops.kv_append(c.k, c.v, c.kv_cache, c.block_table, c.context_lens)
+
+    def call(c, ws=None):
+        out = ops.paged_decode(c.q, c.kv_cache, c.block_table, c.context_lens, s.scale,
+                               s.num_heads, s.num_kv_heads, s.head_dim, workspace=ws)
+        return out.float().cpu()
+
+    ref_small, ref_large = call(small), call(large)
+    assert_close(ref_large, want_large)
+    need = max(ops.decode_workspace_bytes(c.q.shape[0], s.num_heads, s.num_kv_heads,
+                                          s.head_dim, c.block_table.shape[1])
+               for c in (small, large))
+    ws = ops.decode_workspace(need, DEV)
+    for c, ref in ((small, ref_small), (large, ref_large), (small, ref_small),
+                   (large, ref_large), (large, ref_large)):
+        assert torch.equal(call(c, ws), ref)
+    foreign = torch.full((need,), 0x5A, dtype=torch.uint8, device=DEV)
+    assert torch.equal(call(large, foreign), ref_large)
+    assert torch.equal(call(small, foreign), ref_small)
+
+
+def test_graph_replays_of_two_batch_sizes_share_a_workspace():
+    """Captured decodes of 10 and 3 sequences (largest first, as the runner captures its
+    buckets) on one workspace, replayed in mixed order with eager calls of both sizes on
+    the same workspace in between: every replay equals the eager output."""
+    s = wl.LLAMA3_8B
+    large = wl.decode_case(s, [300, 4100, 17, 2500, 9000, 64, 1200, 6000, 0, 800],
+                           seed=210).to(DEV)
+    small = wl.decode_case(s, [5000, 7000, 3000], seed=211).to(DEV)
+    for c in (large, small):
+        ops.kv_append(c.k, c.v, c.kv_cache, c.block_table, c.context_lens)
+
+    def call(c, ws=None):
+        return ops.paged_decode(c.q, c.kv_cache, c.block_table, c.context_lens, s.scale,
+                                s.num_heads, s.num_kv_heads, s.head_dim, workspace=ws)
+
+    refs = {id(c): call(c).float().cpu() for c in (large, small)}
+    need = ops.decode_workspace_bytes(large.q.shape[0], s.num_heads, s.num_kv_heads,
+                                      s.head_dim, max(large.block_table.shape[1],
+                                                      small.block_table.shape[1]))
+    ws = ops.decode_workspace(need, DEV)
+    graphs = {}
+    for c in (large, small):
+        call(c, ws)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = call(c, ws)
+        graphs[id(c)] = (g, out)
+    torch.cuda.synchronize()
+    for c in (small, large, small, small, large, large, small):
+        g, out = graphs[id(c)]
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.float().cpu(), refs[id(c)])
+        other = large if c is small else small
+        assert torch.equal(call(other, ws).float().cpu(), refs[id(other)])
