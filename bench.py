@@ -163,13 +163,23 @@ def extra_measurements(torch, ops, wl, reps):
         ops.paged_decode(c1.q, c1.kv_cache, c1.block_table, c1.context_lens, s1.scale,
                          s1.num_heads, s1.num_kv_heads, s1.head_dim)
     dec1()
-    ms1 = time_region(torch, dec1, reps * 10)
+    ms1_eager = time_region(torch, dec1, reps * 10)
+    layers1 = 24
+
+    def dec1_layers():
+        for _ in range(layers1):
+            dec1()
+    g1 = capture(torch, dec1_layers)
+    ms1 = time_region(torch, g1.replay, reps) / layers1
+    del g1
     b1 = wl.decode_bytes(s1, c1.ctx, c1.block_table.shape[1]) + \
         wl.append_bytes(s1, c1.num_seqs, c1.num_seqs, varlen=False)
     res["qwen2_0.5b_decode"] = {"us_per_layer": round(ms1 * 1e3, 2),
+                                "us_per_layer_eager": round(ms1_eager * 1e3, 2),
                                 "effective_gbs": round(b1 / ms1 / 1e6, 1),
-                                "note": "append + decode of 8 sequences; ~1 MB working set "
-                                        "stays in L2/MALL (cache-resident, not an HBM figure)"}
+                                "note": "append + decode of 8 sequences, 24 layer launches "
+                                        "replayed from one HIP graph; ~1 MB working set stays "
+                                        "in L2/MALL (cache-resident, not an HBM figure)"}
     del c1
 
     # Qwen2-7B varlen prefill: append all prompt tokens, then causal attention.
@@ -357,7 +367,8 @@ def main():
                         "block_size 16, batch 64, context U[512,4096], bf16, random "
                         "non-contiguous block tables, append + paged decode per layer",
             "layers": LAYERS, "batch": len(ctx), "context_tokens": sum(ctx),
-            "num_blocks_per_layer": num_blocks, "partition_tokens": args.partition or "auto (1024 here)",
+            "num_blocks_per_layer": num_blocks, "partition_tokens": args.partition or "auto",
+            "decode_split": "per-sequence workgroups" if ws_bytes <= 256 else "stream split",
         },
         "roofline": {
             "bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,

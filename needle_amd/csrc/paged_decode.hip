@@ -30,6 +30,14 @@
 //     max needs two cross-lane exchanges per block.
 // A second kernel merges the partials of the sequences that span waves and writes
 // zeros for sequences with nothing to attend.
+//
+// Small batches (kv heads x sequences x NW waves within the resident waves, at most 16
+// tiles per wave): one workgroup of NW waves (16 at head_dim 64, 8 at 128) per (kv head,
+// sequence) instead.  Each wave takes 1/NW of the sequence's tiles through the same
+// per-tile code, and the waves
+// combine their (m, l, acc) through LDS: one launch, no workspace traffic.  With few
+// sequences the stream split would cut every sequence into many 2-tile pieces and the
+// merge kernel would cost as much as the attention.
 #include <stdlib.h>
 
 #include "ndl_common.hpp"
@@ -38,6 +46,11 @@ namespace ndl {
 
 // The fewest tiles a wave of the automatic split takes.
 constexpr int kDecodeMinChunk = 2;
+// Waves per workgroup of the per-sequence split (as many as one CU holds at the
+// kernel's register use: 16 at head_dim 64, 8 at 128), and the most tiles per wave for
+// which the automatic choice takes it.
+template <int D> constexpr int seq_split_waves() { return D == 64 ? 16 : 8; }
+constexpr int kSeqSplitMaxTiles = 16;
 
 template <int D> struct VRow;
 template <> struct VRow<128> { using T = u32x4; };  // 8 bf16 per lane per token
@@ -136,21 +149,24 @@ __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
   return c < kDecodeMinChunk ? kDecodeMinChunk : c;
 }
 
-template <int D, int NBUF>
-__global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
+// NW == 1: one wave per workgroup, wave s of a kv head takes stream tiles s*C .. s*C + C.
+// NW > 1: one workgroup per (kv head, sequence); wave w takes tiles w*C .. w*C + C of
+// the sequence (C = ceil(n / NW)) and the waves combine through LDS.
+template <int D, int NBUF, int NW>
+__global__ __launch_bounds__(64 * NW) void paged_decode_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;   // k-steps of the QK^T MFMA
   constexpr int DPL = D / 16;  // head_dim elements per lane per V row
+  constexpr int E = 4 * DPL;   // accumulator elements per lane (head_dim E*j .. + E of head c)
   using VT = typename VRow<D>::T;
 
   // kv head is the fastest grid index: the 8 head slices of one block (adjacent in
   // memory) are fetched by waves dispatched together.
   const int kvh = (int)(blockIdx.x % (unsigned)a.num_kv_heads);
-  const int sw = (int)(blockIdx.x / (unsigned)a.num_kv_heads);   // stream wave of the kv head
-  const int lane = threadIdx.x, j = lane >> 4, c = lane & 15;
+  // NW == 1: stream wave of the kv head; NW > 1: the sequence
+  const int sw = (int)(blockIdx.x / (unsigned)a.num_kv_heads);
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, j = lane >> 4, c = lane & 15;
   const bool head_ok = c < a.group;
   const int head = kvh * a.group + c;
-  const int64_t chunk = stream_chunk(a, lane);
-  const int64_t start = (int64_t)sw * chunk, end = start + chunk;
 
   const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
   const int64_t head_off = (int64_t)kvh * 16 * D;
@@ -161,7 +177,11 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   const int k_row = lane / CPR, k_chunk = lane % CPR;
   const int k_off = k_row * D + 8 * k_chunk;  // + RPI * D * s
   const int v_off = 4 * j * D + DPL * c;      // token rows 4j..4j+3, head_dim DPL*c..
-  __shared__ __attribute__((aligned(16))) u16 ktile[16 * D];
+  // Per wave: a 16 x D K tile; with NW > 1 the same memory later holds each wave's
+  // accumulators ([E][64] floats, twice the tile) for the combine, then (m, l).
+  constexpr int kSmemFloats = NW == 1 ? 8 * D : NW * 64 * E + NW * 32;
+  __shared__ __attribute__((aligned(16))) float smem[kSmemFloats];
+  u16* const ktile = reinterpret_cast<u16*>(smem) + wv * 16 * D;
   // Chunk q of row r lives at r*D + 8*(q ^ swz(r)): conflict-free for both the
   // row-layout writes and the A-operand reads.
   auto swz = [](int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); };
@@ -193,9 +213,12 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
   // The piece that ends a sequence at the start of this wave's tiles is held in registers
   // and stored after the walk: stores count in the same in-order counter as loads, so
   // storing it at once would make the next sequence's first loads wait for the stores.
+  // With NW > 1 the same registers hold this wave's share of its sequence.
   f32x4 held[DPL];
-  float held_m = 0.f, held_l = 0.f;
+  float held_m = kNegInf, held_l = 0.f;
   int held_seg = -1;
+#pragma unroll
+  for (int b = 0; b < DPL; ++b) held[b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Tiles lt0 .. lt1 of sequence seq (n_tiles in all) for the g heads of kv head kvh,
   // as segment segid of this kv head.
@@ -323,7 +346,12 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     if (!head_ok) return;
 
     // acc[b][i] holds O[head c][d = DPL * (4 j + i) + b].
-    if (lt0 == 0 && lt1 == n_tiles) {  // the whole sequence: final output
+    if constexpr (NW > 1) {
+#pragma unroll
+      for (int b = 0; b < DPL; ++b) held[b] = acc[b];
+      held_m = m;
+      held_l = lsum;
+    } else if (lt0 == 0 && lt1 == n_tiles) {  // the whole sequence: final output
       u16* const out_row = a.out + ((int64_t)seq * a.num_heads + head) * D + DPL * 4 * j;
       const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
 #pragma unroll
@@ -348,21 +376,79 @@ __global__ __launch_bounds__(64) void paged_decode_kernel(DecodeArgs a) {
     }
   };
 
-  // Walk the sequences that own tiles start .. end of this kv head's stream.
-  int seq;
-  int64_t first;
-  stream_locate(a, lane, -1, start, &seq, &first);
-  while (seq < a.num_seqs && first < end) {
-    const int nt = seq_tiles(a, seq);
-    if (nt > 0) {
-      const int64_t s0 = start > first ? start : first;
-      const int64_t s1 = end < first + nt ? end : first + nt;
-      segment(seq, (int)(s0 - first), (int)(s1 - first), nt, sw + seq);
+  if constexpr (NW == 1) {
+    // Walk the sequences that own tiles start .. end of this kv head's stream.
+    const int64_t chunk = stream_chunk(a, lane);
+    const int64_t start = (int64_t)sw * chunk, end = start + chunk;
+    int seq;
+    int64_t first;
+    stream_locate(a, lane, -1, start, &seq, &first);
+    while (seq < a.num_seqs && first < end) {
+      const int nt = seq_tiles(a, seq);
+      if (nt > 0) {
+        const int64_t s0 = start > first ? start : first;
+        const int64_t s1 = end < first + nt ? end : first + nt;
+        segment(seq, (int)(s0 - first), (int)(s1 - first), nt, sw + seq);
+      }
+      first += nt;
+      ++seq;
     }
-    first += nt;
-    ++seq;
+    if (held_seg >= 0) store_partial(held_seg, held, held_m, held_l);
+  } else {
+    const int seq = sw;
+    const int nt = seq_tiles(a, seq);
+    const int per = (nt + NW - 1) / NW;
+    const int lt0 = wv * per, lt1 = lt0 + per < nt ? lt0 + per : nt;
+    if (lt0 < lt1) segment(seq, lt0, lt1, nt, 0);
+    // Combine: every wave's (m, l) and accumulators to LDS (the K tiles are dead once
+    // all waves are past their loop), then wave w finishes elements w*KPW .. + KPW of
+    // every lane over the NW waves in a fixed order.  A sequence with nothing to attend
+    // (no tiles) comes out as zeros (attention.py:307-308 on an empty context).
+    constexpr int KPW = E / NW;
+    static_assert(KPW * NW == E, "waves must divide the accumulator elements");
+    float* const sacc = smem;                 // [wave][E][64]
+    float* const sml = smem + NW * 64 * E;    // [wave][2][16]
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+#pragma unroll
+      for (int b = 0; b < DPL; ++b) sacc[(wv * E + DPL * i + b) * 64 + lane] = held[b][i];
+    }
+    if (j == 0) {
+      sml[wv * 32 + c] = held_m;
+      sml[wv * 32 + 16 + c] = held_l;
+    }
+    __syncthreads();
+    if (!head_ok) return;
+    float mx = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sml[w * 32 + c]);
+    float den = 0.f, o[KPW];
+#pragma unroll
+    for (int k = 0; k < KPW; ++k) o[k] = 0.f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      const float mw = sml[w * 32 + c];
+      const float wt = mw == kNegInf ? 0.f : fast_exp2(mw - mx);
+      den += wt * sml[w * 32 + 16 + c];
+#pragma unroll
+      for (int k = 0; k < KPW; ++k) o[k] += wt * sacc[(w * E + wv * KPW + k) * 64 + lane];
+    }
+    const float inv = den > 0.f ? 1.f / den : 0.f;
+    u16* const out_row =
+        a.out + ((int64_t)seq * a.num_heads + head) * D + E * j + wv * KPW;
+    if constexpr (KPW == 1) {
+      out_row[0] = (u16)f32_to_bf16_bits(o[0] * inv);
+    } else {
+      uint32_t w2[KPW / 2];
+#pragma unroll
+      for (int k = 0; k < KPW; k += 2) w2[k / 2] = pack_bf16x2(o[k] * inv, o[k + 1] * inv);
+      if constexpr (KPW == 4)
+        *reinterpret_cast<u32x2*>(out_row) = u32x2{w2[0], w2[1]};
+      else
+        *reinterpret_cast<uint32_t*>(out_row) = w2[0];
+    }
   }
-  if (held_seg >= 0) store_partial(held_seg, held, held_m, held_l);
 }
 
 // Merge of the segment partials: one wave per (query head, sequence).  A sequence
@@ -467,9 +553,10 @@ inline int decode_pipeline_depth() {
   return depth;
 }
 
-// Resident waves of the attention kernel on the current device (CUs times waves per CU),
-// cached per device and kernel; 0 when the device cannot be queried.
-inline int64_t decode_resident_waves(const void* fn) {
+// Resident waves of an attention kernel launched with `block` threads per workgroup on
+// the current device (CUs times workgroups per CU times waves per workgroup), cached per
+// device and kernel; 0 when the device cannot be queried.
+inline int64_t decode_resident_waves(const void* fn, int block = 64) {
   struct Entry { const void* fn; int dev; int64_t waves; };
   static Entry cache[32];
   static int used = 0;
@@ -479,21 +566,22 @@ inline int64_t decode_resident_waves(const void* fn) {
     if (cache[i].fn == fn && cache[i].dev == dev) return cache[i].waves;
   int cus = 0, per_cu = 0;
   if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, 64, 0) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, 0) != hipSuccess ||
       cus <= 0 || per_cu <= 0)
     return 0;
-  const int64_t waves = (int64_t)cus * per_cu;
+  const int64_t waves = (int64_t)cus * per_cu * (block / 64);
   if (used < 32) cache[used++] = Entry{fn, dev, waves};
   return waves;
 }
 
 template <int D> const void* decode_kernel_fn(int depth) {
-  return depth == 2 ? (const void*)paged_decode_kernel<D, 2>
-                    : depth == 4 ? (const void*)paged_decode_kernel<D, 4>
-                                 : (const void*)paged_decode_kernel<D, 3>;
+  return depth == 2 ? (const void*)paged_decode_kernel<D, 2, 1>
+                    : depth == 4 ? (const void*)paged_decode_kernel<D, 4, 1>
+                                 : (const void*)paged_decode_kernel<D, 3, 1>;
 }
 
 struct DecodeLayout {
+  int seq_split;        // waves per (kv head, sequence) workgroup, or 0 for the stream split
   int64_t chunk;        // fixed tiles per wave, or 0 (from the stream length on the device)
   int64_t waves;        // waves per kv head
   int64_t nseg;         // segment slots per kv head
@@ -501,12 +589,40 @@ struct DecodeLayout {
   size_t bytes;         // whole workspace
 };
 
-// Split of the stream.  partition_tokens > 0 (a multiple of 16) fixes the tokens per
-// wave.  Otherwise the launch holds as many waves as can be resident at once, shared
-// by the kv heads, so that every wave that has tiles runs from the start (a device
-// that cannot be queried gets 2048); each takes ceil(T / waves) tiles of its stream.
+// Split of the work.  partition_tokens = -1: one workgroup of seq_split_waves() waves per
+// (kv head, sequence).  partition_tokens > 0 (a multiple of 16): the stream split with
+// that many tokens per wave.  0: the per-sequence workgroups when all of them are
+// resident at once and a sequence of the full table width needs at most
+// kSeqSplitMaxTiles tiles per wave; otherwise the stream split over as many waves as
+// can be resident at once, shared by the kv heads, so that every wave that has tiles
+// runs from the start (a device that cannot be queried counts as 2048 waves); each
+// takes ceil(T / waves) tiles of its stream.
 inline int decode_layout(int num_seqs, int num_heads, int num_kv_heads, int head_dim,
                          int max_blocks, int partition_tokens, DecodeLayout* lay) {
+  lay->seq_split = 0;
+  const int nw = head_dim == 128 ? seq_split_waves<128>() : seq_split_waves<64>();
+  if (partition_tokens == -1) {
+    lay->seq_split = nw;
+  } else if (partition_tokens < 0) {
+    return NDL_ERR_INVALID_ARG;
+  } else if (partition_tokens == 0) {
+    int64_t resident = decode_resident_waves(
+        head_dim == 128 ? (const void*)paged_decode_kernel<128, 2, seq_split_waves<128>()>
+                        : (const void*)paged_decode_kernel<64, 2, seq_split_waves<64>()>,
+        64 * nw);
+    if (resident <= 0) resident = 2048;
+    if ((int64_t)num_kv_heads * num_seqs * nw <= resident &&
+        (max_blocks + nw - 1) / nw <= kSeqSplitMaxTiles)
+      lay->seq_split = nw;
+  }
+  if (lay->seq_split) {  // no partials leave the workgroup
+    lay->chunk = 0;
+    lay->waves = 1;
+    lay->nseg = 0;
+    lay->ml_bytes = 0;
+    lay->bytes = 256;
+    return NDL_OK;
+  }
   if (partition_tokens > 0) {
     if (partition_tokens % 16 != 0) return NDL_ERR_INVALID_ARG;
     lay->chunk = partition_tokens / 16;
@@ -573,9 +689,11 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
   if (rc0 != NDL_OK) return rc0;
   // Segments one sequence can span: its tiles over the chunk, plus the partial ends
   // (the automatic split keeps waves <= kMergeMaxParts - 2).
-  if (lay.chunk > 0 && (int64_t)max_blocks_per_seq / lay.chunk + 2 > kMergeMaxParts)
+  if (!lay.seq_split && lay.chunk > 0 &&
+      (int64_t)max_blocks_per_seq / lay.chunk + 2 > kMergeMaxParts)
     return NDL_ERR_UNSUPPORTED;
-  const int64_t grid_waves = lay.waves * num_kv_heads;
+  const int64_t grid_waves = lay.seq_split ? (int64_t)num_seqs * num_kv_heads
+                                           : lay.waves * num_kv_heads;
   if (grid_waves > 0x7fffffff || lay.nseg > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
   if (workspace == nullptr || workspace_bytes < lay.bytes || ((uintptr_t)workspace & 15u))
     return NDL_ERR_WORKSPACE;
@@ -604,21 +722,31 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
 
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)grid_waves);
+  if (lay.seq_split) {  // one workgroup per (kv head, sequence), kv head fastest
+    const dim3 block(64 * lay.seq_split);
+    if (head_dim == 128)
+      hipLaunchKernelGGL((paged_decode_kernel<128, 2, seq_split_waves<128>()>), grid, block, 0,
+                         s, a);
+    else
+      hipLaunchKernelGGL((paged_decode_kernel<64, 2, seq_split_waves<64>()>), grid, block, 0, s,
+                         a);
+    return check_launch();
+  }
   const int depth = decode_pipeline_depth();
   if (head_dim == 128) {
     if (depth == 2)
-      hipLaunchKernelGGL((paged_decode_kernel<128, 2>), grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((paged_decode_kernel<128, 2, 1>), grid, dim3(64), 0, s, a);
     else if (depth == 4)
-      hipLaunchKernelGGL((paged_decode_kernel<128, 4>), grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((paged_decode_kernel<128, 4, 1>), grid, dim3(64), 0, s, a);
     else
-      hipLaunchKernelGGL((paged_decode_kernel<128, 3>), grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((paged_decode_kernel<128, 3, 1>), grid, dim3(64), 0, s, a);
   } else {
     if (depth == 2)
-      hipLaunchKernelGGL((paged_decode_kernel<64, 2>), grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((paged_decode_kernel<64, 2, 1>), grid, dim3(64), 0, s, a);
     else if (depth == 4)
-      hipLaunchKernelGGL((paged_decode_kernel<64, 4>), grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((paged_decode_kernel<64, 4, 1>), grid, dim3(64), 0, s, a);
     else
-      hipLaunchKernelGGL((paged_decode_kernel<64, 3>), grid, dim3(64), 0, s, a);
+      hipLaunchKernelGGL((paged_decode_kernel<64, 3, 1>), grid, dim3(64), 0, s, a);
   }
   int rc = check_launch();
   if (rc != NDL_OK) return rc;

@@ -198,7 +198,9 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
     """Paged decode attention; same signature as _decode_pytorch (attention.py:291).
 
     Sequence i attends min(context_lens[i] + 1, W * block_size) cached tokens.
-    Returns [num_seqs, num_heads, head_dim] in q's dtype.
+    Returns [num_seqs, num_heads, head_dim] in q's dtype.  partition_tokens: 0 lets the
+    library choose the split; -1 asks for one 8-wave workgroup per (kv head, sequence);
+    a positive multiple of 16 asks for the stream split with that many tokens per wave.
     """
     _check_cache(kv_cache)
     dev = kv_cache.device

@@ -52,12 +52,18 @@ def test_decode_workspace_sizing(lib):
     slots = 8 * (8 + 2) * 4
     ml = (slots * 2 * 4 + 255) // 256 * 256
     assert n == ml + slots * 128 * 4
-    # automatic split: the resident waves of the device (2048 when there is none to
-    # ask) shared by the 8 kv heads; same slot formula
-    n = lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 0)
+    # automatic split, stream form (a table of 257 blocks needs more than 16 tiles per
+    # wave of an 8-wave workgroup): the resident waves of the device (2048 when there is
+    # none to ask) shared by the 8 kv heads; same slot formula
+    n = lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 257, 16, 0)
     fits = [w for w in range(1, 4096)
             if n == (8 * (w + 2) * 4 * 8 + 255) // 256 * 256 + 8 * (w + 2) * 4 * 128 * 4]
     assert len(fits) == 1
+    # one 8-wave workgroup per (kv head, sequence): nothing leaves the workgroup, a
+    # nominal 256 bytes; chosen automatically for 2 x 8 workgroups of 64-block tables
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, -1) == 256
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 0) == 256
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, -2) == 0
     # unsupported block size / partition not a multiple of 16 / heads not a multiple
     assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 32, 256) == 0
     assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 100) == 0

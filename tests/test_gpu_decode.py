@@ -48,10 +48,13 @@ def run_oracle(case):
     return out.float(), pool
 
 
+# partition_tokens: 0 automatic, -1 one 8-wave workgroup per (kv head, sequence), > 0 the
+# stream split with that many tokens per wave.
+@pytest.mark.parametrize("part", [0, -1, 256])
 @pytest.mark.parametrize("cfg", ["qwen2-0.5b-decode", "llama3-8b-decode"])
-def test_decode_named_cases_vs_oracle(cfg):
+def test_decode_named_cases_vs_oracle(cfg, part):
     case = wl.config_case(cfg)
-    got, _ = run_gpu(case)
+    got, _ = run_gpu(case, partition_tokens=part)
     want, pool = run_oracle(case)
     assert_close(got, want)
     s = case.shape
@@ -60,7 +63,7 @@ def test_decode_named_cases_vs_oracle(cfg):
     assert_close(got, ref64)
 
 
-@pytest.mark.parametrize("part", [16, 64, 256, 512, 1024])
+@pytest.mark.parametrize("part", [-1, 16, 64, 256, 512, 1024])
 def test_partition_sizes_agree(part):
     case = wl.decode_case(wl.LLAMA3_8B, [0, 15, 16, 255, 256, 257, 1023, 3000], seed=201)
     got, _ = run_gpu(case, partition_tokens=part)
@@ -72,22 +75,25 @@ def test_partition_sizes_agree(part):
     wl.HeadShape(8, 8, 128), wl.HeadShape(16, 8, 128), wl.HeadShape(28, 4, 128),
     wl.HeadShape(64, 8, 128), wl.HeadShape(16, 1, 128), wl.HeadShape(4, 4, 64),
     wl.HeadShape(14, 2, 64), wl.HeadShape(12, 3, 64), wl.HeadShape(32, 2, 64)])
-def test_group_sizes_and_head_dims(shape):
+@pytest.mark.parametrize("part", [-1, 64])
+def test_group_sizes_and_head_dims(shape, part):
     case = wl.decode_case(shape, [0, 1, 17, 100, 600], seed=202)
-    got, _ = run_gpu(case)
+    got, _ = run_gpu(case, partition_tokens=part)
     want, _ = run_oracle(case)
     assert_close(got, want)
 
 
-def test_single_token_context_is_exact_value_row():
+@pytest.mark.parametrize("part", [-1, 16])
+def test_single_token_context_is_exact_value_row(part):
     case = wl.decode_case(wl.QWEN2_7B, [0, 0, 0, 0], seed=203)
-    got, _ = run_gpu(case)
+    got, _ = run_gpu(case, partition_tokens=part)
     g = case.shape.group
     for h in range(case.shape.num_heads):
         assert torch.equal(got[:, h], case.v[:, h // g].float())
 
 
-def test_row_width_cap():
+@pytest.mark.parametrize("part", [-1, 16])
+def test_row_width_cap(part):
     # context 39 but two table columns: 32 tokens attended, like the reference slice
     # (every slot finite: no append runs here, so the attended slots are pre-filled)
     case = wl.decode_case(wl.LLAMA3_8B, [31, 20], seed=204, garbage=False)
@@ -96,7 +102,7 @@ def test_row_width_cap():
     s = case.shape
     g = case.to(DEV)
     out = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
-                           s.num_heads, s.num_kv_heads, s.head_dim)
+                           s.num_heads, s.num_kv_heads, s.head_dim, partition_tokens=part)
     torch.cuda.synchronize()
     want = paged_ref.decode_pytorch(case.q, case.kv_cache, case.block_table, case.context_lens,
                                     s.scale, s.num_heads, s.num_kv_heads, s.head_dim)
@@ -121,7 +127,7 @@ def test_repeat_calls_are_deterministic():
     assert torch.equal(a, b)
 
 
-@pytest.mark.parametrize("part", [0, 16])
+@pytest.mark.parametrize("part", [-1, 16, 256])
 def test_empty_contexts_give_zeros_between_live_ones(part):
     # context_lens + 1 <= 0: nothing to attend (the reference's empty softmax gives zeros);
     # the neighbours' tiles share the waves those sequences would sit between
@@ -143,7 +149,8 @@ def test_empty_contexts_give_zeros_between_live_ones(part):
     assert_close(got[live], want.float())
 
 
-def test_invalid_block_ids_are_skipped():
+@pytest.mark.parametrize("part", [-1, 64])
+def test_invalid_block_ids_are_skipped(part):
     """A block id outside [0, num_blocks) is never dereferenced: its keys are dropped."""
     shape = wl.LLAMA3_8B
     case = wl.decode_case(shape, [100, 300], seed=207, garbage=False)
@@ -155,7 +162,7 @@ def test_invalid_block_ids_are_skipped():
     s = case.shape
     g = case.to(DEV)
     out = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
-                           s.num_heads, s.num_kv_heads, s.head_dim, partition_tokens=64)
+                           s.num_heads, s.num_kv_heads, s.head_dim, partition_tokens=part)
     torch.cuda.synchronize()
     kvn = case.kv_cache.double().numpy()
     qn = case.q.double().numpy()
@@ -206,27 +213,29 @@ def test_one_workspace_across_calls_and_batch_sizes():
 
 
 def test_graph_replays_of_two_batch_sizes_share_a_workspace():
-    """Captured decodes of 10 and 3 sequences (largest first, as the runner captures its
-    buckets) on one workspace, replayed in mixed order with eager calls of both sizes on
-    the same workspace in between: every replay equals the eager output."""
+    """Captured decodes of 10, 3 and 4 sequences (largest first, as the runner captures
+    its buckets; the last one short enough for the per-sequence workgroups) on one
+    workspace, replayed in mixed order with eager calls on the same workspace in between:
+    every replay equals the eager output."""
     s = wl.LLAMA3_8B
     large = wl.decode_case(s, [300, 4100, 17, 2500, 9000, 64, 1200, 6000, 0, 800],
                            seed=210).to(DEV)
     small = wl.decode_case(s, [5000, 7000, 3000], seed=211).to(DEV)
-    for c in (large, small):
+    tiny = wl.decode_case(s, [100, 40, 300, 1], seed=212).to(DEV)
+    cases = (large, small, tiny)
+    for c in cases:
         ops.kv_append(c.k, c.v, c.kv_cache, c.block_table, c.context_lens)
 
     def call(c, ws=None):
         return ops.paged_decode(c.q, c.kv_cache, c.block_table, c.context_lens, s.scale,
                                 s.num_heads, s.num_kv_heads, s.head_dim, workspace=ws)
 
-    refs = {id(c): call(c).float().cpu() for c in (large, small)}
-    need = ops.decode_workspace_bytes(large.q.shape[0], s.num_heads, s.num_kv_heads,
-                                      s.head_dim, max(large.block_table.shape[1],
-                                                      small.block_table.shape[1]))
+    refs = {id(c): call(c).float().cpu() for c in cases}
+    need = max(ops.decode_workspace_bytes(c.q.shape[0], s.num_heads, s.num_kv_heads,
+                                          s.head_dim, c.block_table.shape[1]) for c in cases)
     ws = ops.decode_workspace(need, DEV)
     graphs = {}
-    for c in (large, small):
+    for c in cases:
         call(c, ws)
         torch.cuda.synchronize()
         g = torch.cuda.CUDAGraph()
@@ -234,10 +243,11 @@ def test_graph_replays_of_two_batch_sizes_share_a_workspace():
             out = call(c, ws)
         graphs[id(c)] = (g, out)
     torch.cuda.synchronize()
-    for c in (small, large, small, small, large, large, small):
+    order = (small, large, tiny, small, large, large, tiny, small)
+    for n, c in enumerate(order):
         g, out = graphs[id(c)]
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out.float().cpu(), refs[id(c)])
-        other = large if c is small else small
+        other = order[(n + 1) % len(order)]
         assert torch.equal(call(other, ws).float().cpu(), refs[id(other)])
