@@ -120,9 +120,11 @@ int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stride,
 
 /*
  * Bytes of scratch ndl_paged_decode needs for this shape (a fixed function of the
- * arguments, 0 for an invalid shape).  partition_tokens = 0 selects the built-in
- * split; a multiple of 16 asks for that many tokens per wave.  Pass the same value
- * to ndl_paged_decode.
+ * arguments and the device, 0 for an invalid shape).  partition_tokens selects the
+ * split: 0 lets the library choose; -1 asks for one workgroup per (kv head, sequence)
+ * whose waves combine their pieces on chip (the workspace is then a nominal 256 bytes);
+ * a positive multiple of 16 asks for the stream split with that many tokens per wave.
+ * Pass the same value to ndl_paged_decode.
  */
 size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
                                         int head_dim, int max_blocks_per_seq, int block_size,
