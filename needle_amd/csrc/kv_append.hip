@@ -4,13 +4,15 @@
 // attention.py:204-246 (_write_kv).  The reference derives the slot of every
 // token with host round trips (context_lens.cpu(), a Python loop of aranges,
 // repeat_interleave) and then issues 2*num_kv_heads index_put_ launches.
-// Here one launch moves both planes: every thread copies one 16-byte chunk
-// of one (token, kv head) row and derives the slot on the device.
+// Here one launch moves both planes: a wave derives the slots of its tokens on the
+// device and its lanes copy the tokens' rows in 16-byte chunks.
 #include "ndl_common.hpp"
 
 namespace ndl {
 
-// Largest i in [0, n) with cu[i] <= t (cu is non-decreasing, cu[0] == 0).
+// Largest i in [0, n) with cu[i] <= t (cu is non-decreasing, cu[0] == 0).  Called with
+// a wave-uniform t, so its loads go through the scalar cache (and their own counter):
+// they proceed while the wave's vector loads are in flight.
 __device__ __forceinline__ int seq_of_token(const int32_t* __restrict__ cu, int n, int64_t t) {
   int lo = 0, hi = n - 1;
   while (lo < hi) {
@@ -20,7 +22,15 @@ __device__ __forceinline__ int seq_of_token(const int32_t* __restrict__ cu, int 
   return lo;
 }
 
-// grid.x covers num_tokens * num_kv_heads * chunks_per_row chunks, grid.y = plane (0 K, 1 V).
+// Tokens per wave at most (all of a wave's loads are issued before its slot lookups and
+// its stores).
+constexpr int kAppendMaxTokensPerWave = 4;
+
+// One wave per group of tokens_per_wave consecutive tokens.  The lanes copy a token's
+// num_kv_heads * head_dim / 8 16-byte chunks of both planes (one 1 KiB instruction per
+// plane when num_kv_heads * head_dim = 512).  The slot of a token is wave-uniform
+// (sequence by binary search over cu_seqlens, position, table column, block), so those
+// lookups go through the scalar cache once per token.
 __global__ __launch_bounds__(256) void kv_append_kernel(
     u16* __restrict__ cache, int64_t plane_elems, int64_t num_blocks, int num_kv_heads,
     int block_size, int head_dim,
@@ -28,40 +38,70 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     const u16* __restrict__ v, int64_t v_tok_stride,
     const int32_t* __restrict__ block_table, int64_t bt_row_stride, int max_blocks,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ context_lens,
-    int num_seqs, int64_t num_tokens) {
-  const int chunks_per_row = head_dim >> 3;
-  const int64_t chunk = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t total = num_tokens * num_kv_heads * chunks_per_row;
-  if (chunk >= total) return;
-  const int plane = blockIdx.y;
+    int num_seqs, int64_t num_tokens, int tokens_per_wave) {
+  const int lane = threadIdx.x & 63;
+  const int64_t wave_id =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int64_t t0 = wave_id * tokens_per_wave;
+  const int cpr = head_dim >> 3;         // chunks per (token, kv head) row
+  const int cpt = num_kv_heads * cpr;    // chunks per token and plane
+  const int64_t packed = cu_seqlens == nullptr ? num_tokens : (int64_t)cu_seqlens[num_seqs];
 
-  const int c = (int)(chunk % chunks_per_row);
-  const int64_t row = chunk / chunks_per_row;
-  const int h = (int)(row % num_kv_heads);
-  const int64_t t = row / num_kv_heads;
-
-  int i;
-  int64_t p;
-  if (cu_seqlens == nullptr) {
-    i = (int)t;
-    p = context_lens[i];
-  } else {
-    if (t >= (int64_t)cu_seqlens[num_seqs]) return;  // tokens past the packed batch
-    i = seq_of_token(cu_seqlens, num_seqs, t);
-    p = (int64_t)context_lens[i] + (t - cu_seqlens[i]);
-  }
-  if (p < 0) return;
-  int64_t col = p / block_size;
-  if (col > max_blocks - 1) col = max_blocks - 1;  // attention.py:144 / :235 clamp
-  const int64_t blk = block_table[(int64_t)i * bt_row_stride + col];
-  if (blk < 0 || blk >= num_blocks) return;
-  const int off = (int)(p % block_size);
-
-  const u16* src = (plane == 0 ? k + t * k_tok_stride : v + t * v_tok_stride)
-                   + (int64_t)h * head_dim + c * 8;
-  u16* dst = cache + plane * plane_elems
-             + ((blk * num_kv_heads + h) * block_size + off) * (int64_t)head_dim + c * 8;
-  st16(dst, ld16(src));
+  // Destination row (element offset in a plane) of each token, or -1 when it is skipped.
+  int64_t dst_row[kAppendMaxTokensPerWave];
+  auto lookup = [&]() {
+#pragma unroll
+    for (int u = 0; u < kAppendMaxTokensPerWave; ++u) {
+      dst_row[u] = -1;
+      const int64_t t = t0 + u;
+      if (u >= tokens_per_wave || t >= num_tokens || t >= packed) continue;
+      int i;
+      int64_t p;
+      if (cu_seqlens == nullptr) {
+        i = (int)t;
+        p = context_lens[i];
+      } else {
+        i = seq_of_token(cu_seqlens, num_seqs, t);
+        p = (int64_t)context_lens[i] + (t - cu_seqlens[i]);
+      }
+      if (p < 0) continue;
+      int64_t col = p / block_size;
+      if (col > max_blocks - 1) col = max_blocks - 1;  // attention.py:144 / :235 clamp
+      const int64_t blk = block_table[(int64_t)i * bt_row_stride + col];
+      if (blk < 0 || blk >= num_blocks) continue;
+      dst_row[u] = (blk * num_kv_heads * block_size + p % block_size) * (int64_t)head_dim;
+    }
+  };
+  // Chunks r*64 .. r*64 + 63 of every token of the wave: all loads, then (round 0) the
+  // slot lookups while the loads are in flight (the source rows depend only on the
+  // token), then the stores.  Lanes past the row's chunks load its last chunk again (no
+  // divergent branch around the loads, so they go out back to back) and store nothing.
+  auto round = [&](const int r, const bool first) {
+    const int cc0 = r * 64 + lane;
+    const bool live = cc0 < cpt;
+    const int cc = live ? cc0 : cpt - 1;
+    const int h = cc / cpr, c = cc - h * cpr;
+    const int64_t in_off = (int64_t)h * head_dim + c * 8;
+    u32x4 kr[kAppendMaxTokensPerWave], vr[kAppendMaxTokensPerWave];
+#pragma unroll
+    for (int u = 0; u < kAppendMaxTokensPerWave; ++u) {
+      if (u < tokens_per_wave && t0 + u < num_tokens) {  // wave-uniform
+        kr[u] = ld16(k + (t0 + u) * k_tok_stride + in_off);
+        vr[u] = ld16(v + (t0 + u) * v_tok_stride + in_off);
+      }
+    }
+    if (first) lookup();
+    const int64_t out_off = ((int64_t)h * block_size) * head_dim + c * 8;
+#pragma unroll
+    for (int u = 0; u < kAppendMaxTokensPerWave; ++u) {
+      if (live && dst_row[u] >= 0) {
+        st16(cache + dst_row[u] + out_off, kr[u]);
+        st16(cache + plane_elems + dst_row[u] + out_off, vr[u]);
+      }
+    }
+  };
+  round(0, true);  // outside the loop: straight-line code, no waits between its loads
+  for (int r = 1; r < (cpt + 63) / 64; ++r) round(r, false);
 }
 
 }  // namespace ndl
@@ -92,14 +132,29 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
   if ((k_tok_stride | v_tok_stride) & 7) return NDL_ERR_INVALID_ARG;
 
   const int64_t plane_elems = num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
-  const int64_t total = num_tokens * num_kv_heads * (head_dim / 8);
-  const int threads = 256;
-  const int64_t blocks = (total + threads - 1) / threads;
+  // As few tokens per wave as keep every wave resident at once (a second, partial round
+  // of waves costs more than longer waves: 17,705 tokens of 4 x 128 went 13.3 us at 1
+  // or 2 tokens per wave, 12.9 us at 3, 14.1 us at 4 on MI355X).
+  static int64_t resident = [] {
+    int dev = 0, cus = 0, per_cu = 0;
+    if (hipGetDevice(&dev) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kv_append_kernel,
+                                                     256, 0) != hipSuccess ||
+        cus <= 0 || per_cu <= 0)
+      return (int64_t)8192;
+    return (int64_t)cus * per_cu * 4;
+  }();
+  int64_t tpw64 = (num_tokens + resident - 1) / resident;
+  const int tpw = (int)(tpw64 < 1 ? 1 : tpw64 > kAppendMaxTokensPerWave ? kAppendMaxTokensPerWave
+                                                                        : tpw64);
+  const int64_t waves = (num_tokens + tpw - 1) / tpw;
+  const int64_t blocks = (waves + 3) / 4;
   if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
-  hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks, 2), dim3(threads), 0,
+  hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      (hipStream_t)stream, (u16*)kv_cache, plane_elems, num_blocks, num_kv_heads,
                      block_size, head_dim, (const u16*)k, k_tok_stride, (const u16*)v,
                      v_tok_stride, block_table, bt_row_stride, max_blocks_per_seq, cu_seqlens,
-                     context_lens, num_seqs, num_tokens);
+                     context_lens, num_seqs, num_tokens, tpw);
   return check_launch();
 }

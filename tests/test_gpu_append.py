@@ -92,3 +92,34 @@ def test_append_fp16_pool():
 def test_decode_append_allocator_tables():
     ctx = [1024, 5000, 77, 2049, 16, 3000]
     _decode_parity(wl.decode_case(wl.LLAMA3_8B, ctx, seed=107, table="allocator"))
+
+
+def test_varlen_append_many_tokens_odd_rows_and_skips():
+    """Enough tokens for 4 tokens per wave: 3 kv heads of head_dim 72 (27 16-byte chunks
+    per row, 81 per token: not a multiple of the 64 lanes), a cached prefix, an empty
+    sequence, two invalid block ids (their tokens are skipped, as the decode kernels skip
+    such blocks) and 7 rows after the packed batch (never written)."""
+    shape = wl.HeadShape(6, 3, 72)
+    case = wl.prefill_case(shape, [1500, 0, 2049, 777, 3], seed=108,
+                           ctx_lens=[0, 5, 17, 1024, 0])
+    nb = case.kv_cache.shape[1]
+    bt = case.block_table.clone()
+    bt[0, 10] = -3
+    bt[2, 50] = nb + 7
+    t, hkv, d = case.k.shape
+    assert t >= 4096
+    extra_k = torch.randn((7, hkv, d)).to(case.k.dtype)
+    extra_v = torch.randn((7, hkv, d)).to(case.v.dtype)
+    want = case.kv_cache.clone()
+    phys, off = paged_ref.slot_of_tokens(bt, case.cu_seqlens, case.context_lens, 16)
+    ok = (phys >= 0) & (phys < nb)
+    assert int((~ok).sum()) == 32
+    for h in range(hkv):
+        want[0, phys[ok], h, off[ok]] = case.k[ok, h]
+        want[1, phys[ok], h, off[ok]] = case.v[ok, h]
+    g = case.to(DEV)
+    kg = torch.cat([g.k, extra_k.to(DEV)])
+    vg = torch.cat([g.v, extra_v.to(DEV)])
+    ops.write_kv(kg, vg, g.kv_cache, bt.to(DEV), g.cu_seqlens, g.context_lens)
+    torch.cuda.synchronize()
+    assert torch.equal(_bits(g.kv_cache.cpu()), _bits(want))
