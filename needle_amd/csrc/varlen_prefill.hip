@@ -319,13 +319,12 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
                                                 bf16x2{(__bf16)1.0f, (__bf16)1.0f}, l_run, false);
       }
     };
-    // O^T += V^T P^T over the step's 32 keys.
-    auto pv = [&](int stage, const uint32_t* pw) {
+    // V^T operands of one step (all 16 transpose reads issued together, ahead of the
+    // exponentials, so that no PV MFMA waits on LDS latency).
+    auto v_reads = [&](int stage, bf16x8* vop) {
       const u16* vt = lv[stage] + vlane;
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pw[4 * t], pw[4 * t + 1],
-                                                           pw[4 * t + 2], pw[4 * t + 3]});
+      for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt) {
           const u16* piece = vt + (t * DT + dt) * 512;
@@ -334,9 +333,18 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
           const i16x4v v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (__attribute__((address_space(3))) i16x4v*)(piece + 8 * 32));
           const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
-          const bf16x8 vop = __builtin_bit_cast(bf16x8, u32x4{w0[0], w0[1], w1[0], w1[1]});
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop, pb, acc[dt], 0, 0, 0);
+          vop[t * DT + dt] = __builtin_bit_cast(bf16x8, u32x4{w0[0], w0[1], w1[0], w1[1]});
         }
+    };
+    // O^T += V^T P^T over the step's 32 keys.
+    auto pv = [&](const bf16x8* vop, const uint32_t* pw) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pw[4 * t], pw[4 * t + 1],
+                                                           pw[4 * t + 2], pw[4 * t + 3]});
+#pragma unroll
+        for (int dt = 0; dt < DT; ++dt)
+          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[t * DT + dt], pb, acc[dt], 0, 0, 0);
       }
     };
 
@@ -364,11 +372,10 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
 
     // One iteration of the ring: QK(step + 1) and the softmax + PV of step.  Its barrier
     // publishes step+1's loads and retires every wave's previous iteration (the last
-    // reader of slot (step - 1) % NS), which then takes step + NS - 1.
-    //   Fast path (no key of the step masked for this wave, no row max moved past the
-    //   slack): one straight-line block, so the QK MFMAs of step+1 interleave with the
-    //   exponentials of step.  Otherwise the slow path masks, rescales, then does the same.
-    //   QK of a step past the last one reads a stale slot; its scores are never used.
+    // reader of slot (step - 1) % NS), which then takes step + NS - 1.  Masking (steps
+    // that reach past a wave's first query position, the tail, invalid blocks) and the
+    // rare rescale are the only branches.  QK of a step past the last one reads a stale
+    // slot; its scores are never used.
     auto iteration = [&](int step, int stage, f32x16& st_cur, f32x16& st_next) {
       const int nstage = stage + 1 == NS ? 0 : stage + 1;
       const bool has_next = step + 1 < nsteps;
@@ -399,33 +406,32 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       mx = half_max(mx);
       const float mx2 = mx * a.scale_log2;
       const bool grow = mx2 > m_run + kRescaleSlack;
+      // Rows whose max grew past the slack move their running max; the accumulator is
+      // scaled in place (tied asm operands: a plain multiply lets the register allocator
+      // give the scaled accumulator new registers and copy it back on every step).
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float m_new = grow ? mx2 : m_run;
+        // 0 when m_run is -inf; rows whose max stays put keep their scale exactly.
+        const float alpha = m_new == m_run ? 1.f : fast_exp2(m_run - m_new);
+#pragma unroll
+        for (int t = 0; t < DT; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i)
+            asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
+        l_run *= alpha;
+        m_run = m_new;
+      }
+      // One straight-line body for every step (the accumulator keeps its registers):
+      // the K reads of step + 1 and the V reads of this step go out first, the
+      // exponentials hide their latency, and the QK MFMAs of step + 1 interleave with them.
       uint32_t pw[8];
       u32x4 ka[KS];
-      if (!masked && __builtin_amdgcn_ballot_w64(grow) == 0) {
-        k_reads(nstage, ka);
-        probs(st, m_run, pw);
-        st_next = qk(ka);
-        pv(stage, pw);
-      } else {
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-          const float m_new = grow ? mx2 : m_run;
-          // 0 when m_run is -inf; rows whose max stays put keep their scale exactly.
-          // In place (tied asm operands): a plain multiply lets the register allocator give
-          // the scaled accumulator new registers and copy it back on every step.
-          const float alpha = m_new == m_run ? 1.f : fast_exp2(m_run - m_new);
-#pragma unroll
-          for (int t = 0; t < DT; ++t)
-#pragma unroll
-            for (int i = 0; i < 16; ++i)
-              asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
-          l_run *= alpha;
-          m_run = m_new;
-        }
-        k_reads(nstage, ka);
-        probs(st, m_run == kNegInf ? 0.f : m_run, pw);
-        st_next = qk(ka);
-        pv(stage, pw);
-      }
+      bf16x8 vop[2 * DT];
+      k_reads(nstage, ka);
+      v_reads(stage, vop);
+      probs(st, m_run == kNegInf ? 0.f : m_run, pw);
+      st_next = qk(ka);
+      pv(vop, pw);
     };
 
     // Ring: steps 0 .. NS-2 in flight at the start; the loop is unrolled by two so that
