@@ -114,6 +114,16 @@ def time_region(torch, fn, reps):
     return e0.elapsed_time(e1) / reps
 
 
+def warm(torch, fn, seconds):
+    """Run fn back to back for about `seconds` (the GPU clock settles for compute-bound
+    kernels after a short ramp; a cold first dispatch reads ~15% slow on the prefill)."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+
+
 def capture(torch, fn):
     """fn() captured as a HIP graph (after one eager call on a side stream to settle it)."""
     side = torch.cuda.Stream()
@@ -193,8 +203,14 @@ def extra_measurements(torch, ops, wl, reps):
         ops.varlen_prefill(c3.q, c3.kv_cache, c3.block_table, c3.cu_seqlens, c3.context_lens,
                            c3.max_seqlen, s3.scale, s3.num_heads, s3.num_kv_heads, s3.head_dim)
     app3()
-    att3()
-    ms_a = time_region(torch, app3, reps)
+    warm(torch, att3, 1.5)
+
+    def app3_x10():
+        for _ in range(10):
+            app3()
+    g3 = capture(torch, app3_x10)   # ~13 us launches: replayed, so host time stays out
+    ms_a = time_region(torch, g3.replay, reps) / 10
+    del g3
     ms_p = time_region(torch, att3, reps)
     t3 = sum(c3.new_lens)
     ab = wl.append_bytes(s3, t3, c3.num_seqs, varlen=True)
@@ -300,6 +316,9 @@ def main():
             torch.cuda.empty_cache()
             c3 = wl.config_case("qwen2-7b-prefill", device=dev, garbage=False)
             s3 = c3.shape
+            warm(torch, lambda: ops.varlen_prefill(
+                c3.q, c3.kv_cache, c3.block_table, c3.cu_seqlens, c3.context_lens,
+                c3.max_seqlen, s3.scale, s3.num_heads, s3.num_kv_heads, s3.head_dim), 1.5)
             for _ in range(args.steps):
                 ops.write_kv(c3.k, c3.v, c3.kv_cache, c3.block_table, c3.cu_seqlens,
                              c3.context_lens)
