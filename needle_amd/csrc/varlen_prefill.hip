@@ -26,9 +26,14 @@
 //   * Software pipeline: QK of step t+1 is issued before the softmax of step t,
 //     so the MFMA pipe works while the VALU computes exponentials.
 //   * fp32 online softmax in the exp2 domain (scale * log2 e folded into one FMA);
-//     the running max is only moved when a row's max grows by more than
-//     kRescaleSlack, so the O^T rescale is rare; the row sums are taken on the
-//     bf16-rounded P (v_dot2_f32_bf16), i.e. on what the PV product consumes.
+//     the exponentials use the running max as it stands, and only a step whose
+//     probabilities could exceed 2^kRescaleSlack (a lane's partial sum above it) or a
+//     row's first attended step takes the exact path (row max, in-place O^T rescale,
+//     exponentials again), so no row max is computed on most steps; the row sums are
+//     taken on the bf16-rounded P (v_dot2_f32_bf16), i.e. on what the PV product
+//     consumes.
+//   * Each step first issues its LDS reads and the QK MFMAs of the next step, which
+//     depend on nothing else in it, then the ring upkeep, masking and softmax.
 //   * Causal masking only on steps that reach past a wave's first query position;
 //     query tiles are dispatched longest-first.
 #include <stdlib.h>
@@ -49,6 +54,8 @@ constexpr int kPrefListLevels = 2048;
 // exp2-domain growth of a row max tolerated before the accumulator is rescaled:
 // probabilities stay <= 2^8, exact in bf16's exponent range and in fp32 sums.
 constexpr float kRescaleSlack = 8.0f;
+// A lane's partial sum of one step's probabilities above this takes the exact path.
+constexpr float kGrowSum = 256.0f;   // 2^kRescaleSlack
 
 struct PrefillArgs {
   u16* out;
@@ -309,14 +316,14 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     };
     // P = exp2(s * scale log2e - m) rounded to bf16 (the B operand of the PV product);
     // the row sum accumulates the rounded values.
-    auto probs = [&](const f32x16& st, float m_use, uint32_t* pw) {
+    auto probs = [&](const f32x16& st, float m_use, uint32_t* pw, float& lsum) {
 #pragma unroll
       for (int r = 0; r < 16; r += 2) {
         const float p0 = fast_exp2(fmaf(st[r], a.scale_log2, -m_use));
         const float p1 = fast_exp2(fmaf(st[r + 1], a.scale_log2, -m_use));
         pw[r >> 1] = pack_bf16x2(p0, p1);
-        l_run = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[r >> 1]),
-                                                bf16x2{(__bf16)1.0f, (__bf16)1.0f}, l_run, false);
+        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[r >> 1]),
+                                               bf16x2{(__bf16)1.0f, (__bf16)1.0f}, lsum, false);
       }
     };
     // V^T operands of one step (all 16 transpose reads issued together, ahead of the
@@ -382,6 +389,16 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       // loads of steps issued after step + 1: min(NS - 3, nsteps - 2 - step)
       if (has_next) wait_loads(nsteps - 2 - step < NS - 3 ? nsteps - 2 - step : NS - 3);
       lds_barrier();
+      // The LDS reads (K of step + 1, V of this step) and the QK MFMAs of step + 1 depend on
+      // nothing below, so they go out first: the matrix core runs while the ring upkeep,
+      // the row max, the growth check and the exponentials of this step run.  The ring
+      // upkeep writes only slots no wave reads in this iteration (the slot of step - 1,
+      // and V of step + 1, which is read after the next barrier).
+      u32x4 ka[KS];
+      bf16x8 vop[2 * DT];
+      k_reads(nstage, ka);
+      v_reads(stage, vop);
+      st_next = qk(ka);
       if (step + NS - 1 < nsteps) stage_in(step + NS - 1, stage == 0 ? NS - 1 : stage - 1);
       if (has_next && needs_vzero(step + 1, nstage)) zero_v(step + 1, nstage);
       const int kv0 = step * kPrefKeys;
@@ -399,38 +416,48 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
           st[r] = ok ? st[r] : kNegInf;
         }
       }
-      float mx = fmaxf(fmaxf(st[0], st[1]), st[2]);
-#pragma unroll
-      for (int r = 3; r < 15; r += 2) mx = fmaxf(fmaxf(mx, st[r]), st[r + 1]);
-      mx = fmaxf(mx, st[15]);
-      mx = half_max(mx);
-      const float mx2 = mx * a.scale_log2;
-      const bool grow = mx2 > m_run + kRescaleSlack;
-      // Rows whose max grew past the slack move their running max; the accumulator is
-      // scaled in place (tied asm operands: a plain multiply lets the register allocator
-      // give the scaled accumulator new registers and copy it back on every step).
-      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float m_new = grow ? mx2 : m_run;
-        // 0 when m_run is -inf; rows whose max stays put keep their scale exactly.
-        const float alpha = m_new == m_run ? 1.f : fast_exp2(m_run - m_new);
-#pragma unroll
-        for (int t = 0; t < DT; ++t)
-#pragma unroll
-          for (int i = 0; i < 16; ++i)
-            asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
-        l_run *= alpha;
-        m_run = m_new;
-      }
-      // One straight-line body for every step (the accumulator keeps its registers):
-      // the K reads of step + 1 and the V reads of this step go out first, the
-      // exponentials hide their latency, and the QK MFMAs of step + 1 interleave with them.
+      // Exponentials against the running max as it stands.  A row whose max grew by
+      // more than the slack has some p > 2^slack, so its lane's partial sum of the step
+      // exceeds 2^slack; then (and while a row has no running max yet, i.e. at its first
+      // attended step) the wave takes the exact path: row max, in-place rescale, the
+      // exponentials again.  No row max is computed otherwise.  (A sum past the bound
+      // without such a p only costs an early rescale.)
       uint32_t pw[8];
-      u32x4 ka[KS];
-      bf16x8 vop[2 * DT];
-      k_reads(nstage, ka);
-      v_reads(stage, vop);
-      probs(st, m_run == kNegInf ? 0.f : m_run, pw);
-      st_next = qk(ka);
+      float lstep = 0.f;
+      probs(st, m_run == kNegInf ? 0.f : m_run, pw, lstep);
+      const bool exact = !(lstep <= kGrowSum) || m_run == kNegInf;
+      if (__builtin_amdgcn_ballot_w64(exact) != 0) {
+        float m3[6];  // row max as a tree (three levels of 3-input max)
+#pragma unroll
+        for (int i = 0; i < 5; ++i) m3[i] = fmaxf(fmaxf(st[3 * i], st[3 * i + 1]), st[3 * i + 2]);
+        m3[5] = st[15];
+        float mx = fmaxf(fmaxf(fmaxf(m3[0], m3[1]), m3[2]), fmaxf(fmaxf(m3[3], m3[4]), m3[5]));
+        mx = half_max(mx);
+        const float m_new = fmaxf(m_run, mx * a.scale_log2);
+        if (m_new != m_run) {
+          // The accumulator is scaled in place (tied asm operands: a plain multiply lets
+          // the register allocator give the scaled accumulator new registers and copy it
+          // back on every step).  0 when m_run is -inf (nothing accumulated yet).
+          const float alpha = fast_exp2(m_run - m_new);
+          // The compiler's hazard tracking does not look into inline asm: the first
+          // multiply carries the wait state a VALU read of a transcendental's result
+          // needs (without it, it reads the register's previous contents).
+#pragma unroll
+          for (int t = 0; t < DT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+              if (t == 0 && i == 0)
+                asm volatile("s_nop 1\n\tv_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
+              else
+                asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
+            }
+          l_run *= alpha;
+          m_run = m_new;
+        }
+        lstep = 0.f;
+        probs(st, m_run == kNegInf ? 0.f : m_run, pw, lstep);
+      }
+      l_run += lstep;
       pv(vop, pw);
     };
 
