@@ -247,17 +247,24 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     // Stage `step` into ring slot `stage`: note its block validity and, on loader waves,
     // issue its direct loads.  An invalid block id reads block 0 instead (always mapped);
     // rows past the range read whatever the table maps them to.  The softmax masks both.
+    // A window of the table with no invalid id (the normal case) sets no bits, and then
+    // only the loader waves read block ids.
+    bool win_bad = false;
     auto stage_in = [&](int step, int stage) {
       const int c0 = clamp_col(2 * step), c1 = clamp_col(2 * step + 1);  // same 64-window
       if (c0 < win0 || c0 >= win0 + 64) {
         win0 = c0 & ~63;
         btw = win0 + lane < a.max_blocks ? bt_row[win0 + lane] : 0;
         vm_wait<0>();
+        win_bad = __builtin_amdgcn_ballot_w64(win0 + lane < a.max_blocks &&
+                                              (uint32_t)btw >= nb32) != 0;
       }
+      badbits &= ~(3u << (2 * stage));
+      if (!loader && !win_bad) return;
       const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane(btw, c0 - win0);
       const uint32_t b1 = (uint32_t)__builtin_amdgcn_readlane(btw, c1 - win0);
-      const uint32_t bad = (b0 >= nb32 ? 1u : 0u) | (b1 >= nb32 ? 2u : 0u);
-      badbits = (badbits & ~(3u << (2 * stage))) | (bad << (2 * stage));
+      if (win_bad)
+        badbits |= ((b0 >= nb32 ? 1u : 0u) | (b1 >= nb32 ? 2u : 0u)) << (2 * stage);
       if (!loader) return;
       const uint32_t b = ld_blk ? b1 : b0;
       const u16* base = ld_head + (int64_t)(b < nb32 ? b : 0u) * blk_stride;
