@@ -81,73 +81,91 @@ struct RopeArgs {
   int64_t num_tokens;
 };
 
-// Element offset of (token t, kv head h) in the K plane, by the append's slot rule
-// (attention.py:143-146, :224-237); false when the slot is out of range.
-__device__ __forceinline__ bool kv_slot(const RopeArgs& a, int64_t t, int h, int64_t& off) {
+// Element offset in a plane of (token t, kv head 0)'s slot by the append's rule
+// (attention.py:143-146, :224-237), or -1 when the slot is out of range.  t is
+// wave-uniform, so these loads go through the scalar cache.
+__device__ __forceinline__ int64_t kv_slot_row(const RopeArgs& a, int64_t t) {
   int i;
   int64_t p;
   if (a.cu_seqlens == nullptr) {
     i = (int)t;
     p = a.context_lens[i];
   } else {
-    if (t >= (int64_t)a.cu_seqlens[a.num_seqs]) return false;
+    if (t >= (int64_t)a.cu_seqlens[a.num_seqs]) return -1;
     i = seq_of_token_rope(a.cu_seqlens, a.num_seqs, t);
     p = (int64_t)a.context_lens[i] + (t - a.cu_seqlens[i]);
   }
-  if (p < 0) return false;
+  if (p < 0) return -1;
   int64_t col = p / a.block_size;
   if (col > a.max_blocks - 1) col = a.max_blocks - 1;
   const int64_t blk = a.block_table[(int64_t)i * a.bt_row_stride + col];
-  if (blk < 0 || blk >= a.num_blocks) return false;
-  off = ((blk * a.num_kv_heads + h) * a.block_size + p % a.block_size) * (int64_t)a.head_dim;
-  return true;
+  if (blk < 0 || blk >= a.num_blocks) return -1;
+  return (blk * a.num_kv_heads * a.block_size + p % a.block_size) * (int64_t)a.head_dim;
 }
 
-// One thread per (token, row, 8-element chunk of the first half).  Rows 0..H-1 are q
-// heads, H..H+Hkv-1 k heads, H+Hkv..H+2Hkv-1 v heads (copied, not rotated).
+// One wave per (token, round of 64 items).  A token's items are its (row, 8-element
+// chunk of the first half) pairs: first the 2 * Hkv k and v rows (k rotated into the K
+// plane, v copied into the V plane), then the H q rows (rotated into q_out).  Every wave
+// runs one straight-line round: its loads go out first, then (k/v rounds) the slot
+// lookup, which comes before any store of the kernel and so reads through the scalar
+// cache.  Lanes past the last item load a valid item again and store nothing, so no
+// divergent branch separates the loads.  (A lane chooses between two row bases at most:
+// a three-way choice of pointers compiles to a lookup table in scratch memory.)
 __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
-  const int half = a.head_dim >> 1;
-  const int cph = half >> 3;  // chunks per half row
-  const int rows = a.num_heads + 2 * a.num_kv_heads;
-  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (idx >= a.num_tokens * rows * cph) return;
-  const int c = (int)(idx % cph);
-  const int64_t rt = idx / cph;
-  const int row = (int)(rt % rows);
-  const int64_t t = rt / rows;
-  const int d0 = 8 * c;
+  const int lane = threadIdx.x & 63;
+  const int64_t w =
+      (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
+  const int D = a.head_dim, half = D >> 1, cph = half >> 3;  // chunks per half row
+  const int H = a.num_heads, Hkv = a.num_kv_heads, bs = a.block_size;
+  const int kv_items = 2 * Hkv * cph, q_items = H * cph;
+  const int kv_rounds = (kv_items + 63) >> 6, rounds = kv_rounds + ((q_items + 63) >> 6);
+  const int64_t t = w / rounds;
+  const int r = (int)(w - t * rounds);
+  if (t >= a.num_tokens) return;  // wave-uniform
+  const u16* const cs = a.cos + t * a.cs_tok_stride;
+  const u16* const sn = a.sin + t * a.cs_tok_stride;
 
-  if (row >= a.num_heads + a.num_kv_heads) {  // v: both halves copied into the V plane
-    const int h = row - a.num_heads - a.num_kv_heads;
-    int64_t off;
-    if (!kv_slot(a, t, h, off)) return;
-    const u16* src = a.v + t * a.v_tok_stride + (int64_t)h * a.head_dim;
-    u16* dst = a.cache + a.plane_elems + off;
-    st16(dst + d0, ld16(src + d0));
-    st16(dst + d0 + half, ld16(src + d0 + half));
-    return;
+  if (r < kv_rounds) {  // k / v rows
+    const int item0 = 64 * r + lane;
+    const bool live = item0 < kv_items;
+    const int item = live ? item0 : kv_items - 1;
+    const int row = item / cph, c = item - row * cph, d0 = 8 * c;
+    const bool is_v = row >= Hkv;
+    const int h = is_v ? row - Hkv : row;
+    const u16* src = (is_v ? a.v + t * a.v_tok_stride : a.k + t * a.k_tok_stride) +
+                     (int64_t)h * D;
+    const u32x4 lo = ld16(src + d0), hi = ld16(src + d0 + half);
+    const u32x4 clo = ld16(cs + d0), chi = ld16(cs + d0 + half);
+    const u32x4 slo = ld16(sn + d0), shi = ld16(sn + d0 + half);
+    const int64_t krow = kv_slot_row(a, t);
+    u32x4 olo, ohi;
+    rope8(lo, hi, clo, chi, slo, shi, olo, ohi);
+    if (is_v) {
+      olo = lo;
+      ohi = hi;
+    }
+    if (live && krow >= 0) {
+      u16* const dst = a.cache + (is_v ? a.plane_elems : 0) + krow + (int64_t)h * bs * D;
+      st16(dst + d0, olo);
+      st16(dst + d0 + half, ohi);
+    }
+  } else {  // q rows
+    const int item0 = 64 * (r - kv_rounds) + lane;
+    const bool live = item0 < q_items;
+    const int item = live ? item0 : q_items - 1;
+    const int row = item / cph, c = item - row * cph, d0 = 8 * c;
+    const u16* src = a.q + t * a.q_tok_stride + (int64_t)row * D;
+    const u32x4 lo = ld16(src + d0), hi = ld16(src + d0 + half);
+    const u32x4 clo = ld16(cs + d0), chi = ld16(cs + d0 + half);
+    const u32x4 slo = ld16(sn + d0), shi = ld16(sn + d0 + half);
+    u32x4 olo, ohi;
+    rope8(lo, hi, clo, chi, slo, shi, olo, ohi);
+    if (live) {
+      u16* const dst = a.q_out + (t * H + row) * (int64_t)D;
+      st16(dst + d0, olo);
+      st16(dst + d0 + half, ohi);
+    }
   }
-
-  const u16* cs = a.cos + t * a.cs_tok_stride;
-  const u16* sn = a.sin + t * a.cs_tok_stride;
-  const u32x4 clo = ld16(cs + d0), chi = ld16(cs + d0 + half);
-  const u32x4 slo = ld16(sn + d0), shi = ld16(sn + d0 + half);
-  u32x4 olo, ohi;
-  u16* dst;
-  const u16* src;
-  if (row < a.num_heads) {  // q: rotated into q_out [T][H][D]
-    src = a.q + t * a.q_tok_stride + (int64_t)row * a.head_dim;
-    dst = a.q_out + (t * a.num_heads + row) * (int64_t)a.head_dim;
-  } else {                  // k: rotated into its K-plane slot
-    const int h = row - a.num_heads;
-    int64_t off;
-    if (!kv_slot(a, t, h, off)) return;
-    src = a.k + t * a.k_tok_stride + (int64_t)h * a.head_dim;
-    dst = a.cache + off;
-  }
-  rope8(ld16(src + d0), ld16(src + d0 + half), clo, chi, slo, shi, olo, ohi);
-  st16(dst + d0, olo);
-  st16(dst + d0 + half, ohi);
 }
 
 }  // namespace ndl
@@ -206,8 +224,10 @@ extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stri
   a.context_lens = context_lens;
   a.num_seqs = num_seqs;
   a.num_tokens = num_tokens;
-  const int64_t total = num_tokens * (num_heads + 2 * num_kv_heads) * (head_dim / 16);
-  const int64_t blocks = (total + 255) / 256;
+  // one wave per (token, round of 64 items), 4 per workgroup
+  const int64_t cph = head_dim / 16;
+  const int64_t rounds = (2 * num_kv_heads * cph + 63) / 64 + (num_heads * cph + 63) / 64;
+  const int64_t blocks = (num_tokens * rounds + 3) / 4;
   if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
   hipLaunchKernelGGL(rope_kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0,
                      (hipStream_t)stream, a);
