@@ -56,6 +56,7 @@ constexpr int kPrefListLevels = 2048;
 constexpr float kRescaleSlack = 8.0f;
 // A lane's partial sum of one step's probabilities above this takes the exact path.
 constexpr float kGrowSum = 256.0f;   // 2^kRescaleSlack
+static_assert(kGrowSum == (float)(1 << (int)kRescaleSlack), "growth bound is 2^slack");
 
 struct PrefillArgs {
   u16* out;
@@ -80,6 +81,14 @@ struct PrefillArgs {
   int64_t num_tokens;
   int num_seqs;
   int persistent;     // 1: grid of resident workgroups walking the tile list
+};
+
+// One query tile, resolved one tile ahead by the persistent walk: rows
+// qtile * wg_rows .. of sequence seq (tokens tok0 .., n rows, ctx cached tokens before
+// them), kv head kvh, head chunk chunk.  n == 0: nothing to compute.
+struct PrefTile {
+  int64_t tok0;
+  int seq, qtile, kvh, chunk, n, ctx;
 };
 
 typedef __attribute__((ext_vector_type(16))) float f32x16;
@@ -111,6 +120,13 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_barrier" ::: "me
 __device__ __forceinline__ void lds_dma16(const void* gbase, uint32_t lane_off,
                                           uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(lane_off), "s"(gbase)
+               : "memory", "m0");
+}
+// The same with one dword per lane, landing at lds_addr + 4 * L.
+__device__ __forceinline__ void lds_dma4(const void* gbase, uint32_t lane_off, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dword %1, %2"
                :
                : "s"(__builtin_amdgcn_readfirstlane(lds_addr)), "v"(lane_off), "s"(gbase)
                : "memory", "m0");
@@ -154,11 +170,13 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   constexpr int PIECES = kPrefKeys / RPP;                 // pieces per plane per step
   constexpr int IPW = 2 * PIECES / kPrefLoaders;          // loads per loader wave per step
   static_assert(IPW >= 1 && (2 * PIECES) % kPrefLoaders == 0, "load distribution");
-  static_assert(NS >= 3 && NS - 2 <= 6 && (NS - 2) * IPW < 64, "ring depth");
+  static_assert(NS >= 5 && NS - 3 <= 6 && (NS - 3) * IPW < 64, "ring depth");
+  static_assert(2 * NS - 3 >= kPrefMaxWaves, "an output piece per wave");
 
   // Ring of NS steps; each stage holds 32 K rows and 32 V rows.
   __shared__ __attribute__((aligned(16))) u16 lk[NS][kPrefKeys * D];
   __shared__ __attribute__((aligned(16))) u16 lv[NS][kPrefKeys * D];
+  __shared__ uint32_t lds_sink[64];   // destination of the L2 warm-up loads, never read
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
@@ -167,21 +185,34 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   const int r32 = lane & 31, h = lane >> 5;
   const int wg_rows = kPrefRows * a.subtiles;
 
-  // One query tile: rows qtile * wg_rows .. of sequence seq, kv head kvh, head chunk
-  // chunk.  Every wave of the workgroup runs it together (it has workgroup barriers).
-  auto tile = [&](const int seq, const int qtile, const int kvh, const int chunk) {
-    const int hg = chunk * a.heads_per_wg + hw;                  // head within the group
-    const int head = kvh * a.group + hg;
-
-    // Rows past num_tokens are never touched, whatever cu_seqlens holds.
+  // Sequence bounds of a tile (scalar loads).  Rows past num_tokens are never touched,
+  // whatever cu_seqlens holds.
+  auto resolve = [&](int seq, int qtile, int kvh, int chunk) {
+    PrefTile t{0, seq, qtile, kvh, chunk, 0, 0};
     const int64_t tok0 = a.cu_seqlens[seq];
     int64_t tok1 = a.cu_seqlens[seq + 1];
     if (tok1 > a.num_tokens) tok1 = a.num_tokens;
-    if (tok0 < 0 || tok1 <= tok0) return;
-    const int n = (int)(tok1 - tok0);
-    const int row0 = qtile * wg_rows;
-    if (row0 >= n) return;
-    const int ctx = a.context_lens[seq] < 0 ? 0 : a.context_lens[seq];
+    if (tok0 < 0 || tok1 <= tok0 || (int64_t)qtile * wg_rows >= tok1 - tok0) return t;
+    t.tok0 = tok0;
+    t.n = (int)(tok1 - tok0);
+    t.ctx = a.context_lens[seq] < 0 ? 0 : a.context_lens[seq];
+    return t;
+  };
+
+  // One query tile (see PrefTile).  Every wave of the workgroup runs it together (it has
+  // workgroup barriers).  ahead() resolves nx, the tile this workgroup takes next
+  // (n == 0: none); it runs while the tile's first loads are in flight, and nx's Q rows
+  // and table window are pulled into the L2 at the end of this tile.
+  auto tile = [&](const PrefTile& t, const PrefTile& nx, auto&& ahead) {
+    if (t.n <= 0) {
+      ahead();
+      return;
+    }
+    const int seq = t.seq, kvh = t.kvh, n = t.n, ctx = t.ctx;
+    const int64_t tok0 = t.tok0;
+    const int hg = t.chunk * a.heads_per_wg + hw;                // head within the group
+    const int head = kvh * a.group + hg;
+    const int row0 = t.qtile * wg_rows;
     const int kv_end = ctx + (row0 + wg_rows < n ? row0 + wg_rows : n);
     const int nsteps = (kv_end + kPrefKeys - 1) / kPrefKeys;
 
@@ -189,6 +220,18 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     const bool wave_active = wrow0 < n && hg < a.group && sub < a.subtiles;
     const int qpos_min = ctx + wrow0;
     const int qpos = ctx + wrow0 + r32;                          // this lane's query position
+
+    const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
+    const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
+    // Block ids are int32; every id in [0, nb32) is a valid block.
+    const uint32_t nb32 = a.num_blocks > 0x7fffffff ? 0x80000000u : (uint32_t)a.num_blocks;
+
+    // Block ids come from a 64-entry window of the table row held one per lane and are
+    // read with readlane (uniform).  The first window goes out with the Q loads below
+    // and one wait covers both; a later refill waits for every outstanding load (a
+    // vector-memory wait cannot single one out); it happens once per 64 blocks.
+    int win0 = 0;
+    int btw = lane < a.max_blocks ? bt_row[lane] : 0;
 
     // B operand of S^T = K Q^T: lane l supplies Q[row l%32][16 s + 8 h .. + 8).
     bf16x8 qb[KS];
@@ -202,14 +245,11 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
         qb[s] = __builtin_bit_cast(bf16x8, w);
       }
     }
-    // Retire the Q loads before the ring starts, so that no wait inside the loop has to
-    // cover them (the ring's own waits count only its direct loads).
+    ahead();
+    // Retire the Q and table loads (and the previous tile's L2 warm-up loads) before the
+    // ring starts, so that no wait inside the loop has to cover them (the ring's own
+    // waits count only its direct loads).
     vm_wait<0>();
-
-    const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
-    const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
-    // Block ids are int32; every id in [0, nb32) is a valid block.
-    const uint32_t nb32 = a.num_blocks > 0x7fffffff ? 0x80000000u : (uint32_t)a.num_blocks;
 
     // Loader waves 0..3 stage, per step, plane (w >> 1) (K, V) of block (w & 1) of the
     // step: IPW direct loads of 1 KiB each, into pieces (w & 1) * IPW + e of that plane.
@@ -235,10 +275,6 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     const uint32_t lds_k0 = lds_addr(&lk[0][0]), lds_v0 = lds_addr(&lv[0][0]);
     const uint32_t ld_lds = (ld_plane ? lds_v0 : lds_k0) + ld_blk * IPW * 1024;
 
-    // Block ids come from a 64-entry window of the table row held one per lane and are
-    // read with readlane (uniform).  A window refill waits for every outstanding load
-    // (a vector-memory wait cannot single one out); it happens once per 64 blocks.
-    int win0 = -64, btw = 0;
     auto clamp_col = [&](int col) { return col > a.max_blocks - 1 ? a.max_blocks - 1 : col; };
     // bit 2*stage + b: block b of that stage's step is not a valid id.  Every wave keeps
     // its own copy (all waves walk the same table window).
@@ -249,7 +285,7 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     // rows past the range read whatever the table maps them to.  The softmax masks both.
     // A window of the table with no invalid id (the normal case) sets no bits, and then
     // only the loader waves read block ids.
-    bool win_bad = false;
+    bool win_bad = __builtin_amdgcn_ballot_w64(lane < a.max_blocks && (uint32_t)btw >= nb32) != 0;
     auto stage_in = [&](int step, int stage) {
       const int c0 = clamp_col(2 * step), c1 = clamp_col(2 * step + 1);  // same 64-window
       if (c0 < win0 || c0 >= win0 + 64) {
@@ -384,30 +420,66 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       }
     };
 
-    // One iteration of the ring: QK(step + 1) and the softmax + PV of step.  Its barrier
-    // publishes step+1's loads and retires every wave's previous iteration (the last
-    // reader of slot (step - 1) % NS), which then takes step + NS - 1.  Masking (steps
-    // that reach past a wave's first query position, the tail, invalid blocks) and the
-    // rare rescale are the only branches.  QK of a step past the last one reads a stale
-    // slot; its scores are never used.
-    auto iteration = [&](int step, int stage, f32x16& st_cur, f32x16& st_next) {
-      const int nstage = stage + 1 == NS ? 0 : stage + 1;
-      const bool has_next = step + 1 < nsteps;
-      // loads of steps issued after step + 1: min(NS - 3, nsteps - 2 - step)
-      if (has_next) wait_loads(nsteps - 2 - step < NS - 3 ? nsteps - 2 - step : NS - 3);
+    // The ring walks the steps two at a time (trip t: steps t, t + 1).  At the start of
+    // a trip, steps up to min(t + NS - 3, nsteps - 1) have their loads issued and V rows
+    // of steps up to t are cleared where needed.  A trip normally has one barrier, before
+    // step t: it publishes steps t + 1 and t + 2 (K of step t + 2 is read by step t + 1),
+    // retires every wave's reads of steps before t, whose slots then take steps
+    // t + NS - 2 and t + NS - 1, and clears V rows of step t + 2.  A trip whose second step
+    // has V rows to clear (the last step, steps over invalid block ids) takes a second
+    // barrier before step t + 1 instead.
+    //   kPair:  barrier publishing t + 1, t + 2; issues t + NS - 2, t + NS - 1
+    //   kFirst: barrier publishing t + 1;        issues t + NS - 2, t + NS - 1
+    //   kSecond (step t + 1): barrier publishing t + 2; also the last step of an odd
+    //           count, whose loads the trip before waited for and whose V rows it
+    //           cleared (the barrier publishes the clearing)
+    //   kNone:  no barrier (second step of a paired trip)
+    enum { kNone = 0, kPair = 1, kFirst = 2, kSecond = 3 };
+    auto slot_after = [](int stage, int k) { return stage + k >= NS ? stage + k - NS : stage + k; };
+    // Returns the last step the barrier publishes (`step` itself when there is none).
+    auto sync = [&](int step, int mode) {
+      const int lead = step + (mode == kPair ? 2 : 1);
+      const int need = lead < nsteps - 1 ? lead : nsteps - 1;
+      if (loader && need > step) {
+        // steps issued at the barrier before this one, counted from `step`
+        const int ahead = step + (mode == kSecond ? NS - 2 : NS - 3);
+        const int later = (ahead < nsteps - 1 ? ahead : nsteps - 1) - need;
+        if (later == NS - 5) vm_wait<(NS - 5) * IPW>();   // a paired trip in full flow
+        else wait_loads(later);
+      }
       lds_barrier();
+      return need;
+    };
+    auto upkeep = [&](int step, int stage, int need, int mode) {
+      if (mode != kSecond) {
+        if (step + NS - 2 < nsteps) stage_in(step + NS - 2, slot_after(stage, NS - 2));
+        if (step + NS - 1 < nsteps) stage_in(step + NS - 1, slot_after(stage, NS - 1));
+      }
+      if (need > step) {
+        const int ns = slot_after(stage, need - step);
+        if (needs_vzero(need, ns)) zero_v(need, ns);
+      }
+    };
+
+    // One step: QK(step + 1) and the softmax + PV of step, after the trip's barrier if
+    // `mode` has one.  Masking (steps that reach past a wave's first query position, the
+    // tail, invalid blocks) and the rare rescale are the only other branches.  QK of a
+    // step past the last one reads a stale slot; its scores are never used.
+    auto iteration = [&](int step, int stage, f32x16& st_cur, f32x16& st_next, int mode) {
+      const int nstage = stage + 1 == NS ? 0 : stage + 1;
+      int need = 0;
+      if (mode != kNone) need = sync(step, mode);
       // The LDS reads (K of step + 1, V of this step) and the QK MFMAs of step + 1 depend on
       // nothing below, so they go out first: the matrix core runs while the ring upkeep,
-      // the row max, the growth check and the exponentials of this step run.  The ring
-      // upkeep writes only slots no wave reads in this iteration (the slot of step - 1,
-      // and V of step + 1, which is read after the next barrier).
+      // the row max, the growth check and the exponentials of this step run.  The upkeep
+      // writes only slots no wave reads before the next barrier: those of steps before
+      // this one, and V of step `need`, read after it.
       u32x4 ka[KS];
       bf16x8 vop[2 * DT];
       k_reads(nstage, ka);
       v_reads(stage, vop);
       st_next = qk(ka);
-      if (step + NS - 1 < nsteps) stage_in(step + NS - 1, stage == 0 ? NS - 1 : stage - 1);
-      if (has_next && needs_vzero(step + 1, nstage)) zero_v(step + 1, nstage);
+      if (mode != kNone) upkeep(step, stage, need, mode);
       const int kv0 = step * kPrefKeys;
       const bool masked = kv0 + kPrefKeys - 1 > qpos_min || kv0 + kPrefKeys > kv_end ||
                           ((badbits >> (2 * stage)) & 3u) != 0;
@@ -468,14 +540,13 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       pv(vop, pw);
     };
 
-    // Ring: steps 0 .. NS-2 in flight at the start; the loop is unrolled by two so that
-    // the two score tiles alternate without copies.  The barrier retires every wave's
-    // reads of the previous tile (persistent launch) before the slots are refilled.
+    // Ring: steps 0 .. NS-3 in flight at the start.  The first barrier retires every
+    // wave's reads of the previous tile (persistent launch) before the slots are refilled.
     lds_barrier();
 #pragma unroll
-    for (int t = 0; t < NS - 1; ++t)
+    for (int t = 0; t < NS - 2; ++t)
       if (t < nsteps) stage_in(t, t);
-    wait_loads(nsteps - 1 < NS - 2 ? nsteps - 1 : NS - 2);
+    wait_loads(nsteps - 1 < NS - 3 ? nsteps - 1 : NS - 3);
     lds_barrier();
     if (needs_vzero(0, 0)) zero_v(0, 0);
     f32x16 st0, st1;
@@ -486,32 +557,89 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     }
     int step = 0, stage = 0;
     for (; step + 2 <= nsteps; step += 2) {
-      iteration(step, stage, st0, st1);
-      stage = stage + 1 == NS ? 0 : stage + 1;
-      iteration(step + 1, stage, st1, st0);
-      stage = stage + 1 == NS ? 0 : stage + 1;
+      const int stage1 = stage + 1 == NS ? 0 : stage + 1;
+      const bool pair = !needs_vzero(step + 1, stage1);
+      iteration(step, stage, st0, st1, pair ? kPair : kFirst);
+      iteration(step + 1, stage1, st1, st0, pair ? kNone : kSecond);
+      stage = stage1 + 1 == NS ? 0 : stage1 + 1;
     }
-    if (step < nsteps) iteration(step, stage, st0, st1);
+    if (step < nsteps) iteration(step, stage, st0, st1, kSecond);  // a barrier, no loads
+
+    // Pull the next tile's Q rows of this wave and (wave 0) its table window into the
+    // L2, after the ring's last wait: direct loads into a scratch LDS word per lane that
+    // nothing reads, retired by the next tile's first wait.  Lane l touches row l / 2,
+    // 128-byte half l % 2 of the row's head slice.
+    if (nx.n > 0) {
+      const int nrow0 = nx.qtile * wg_rows + sub * kPrefRows;
+      const int nhg = nx.chunk * a.heads_per_wg + hw;
+      if (nrow0 < nx.n && nhg < a.group && sub < a.subtiles) {
+        const int r = nrow0 + (lane >> 1) < nx.n ? lane >> 1 : 0;
+        const u16* base = a.q + (nx.tok0 + nrow0) * a.q_tok_stride +
+                          (int64_t)(nx.kvh * a.group + nhg) * D;
+        lds_dma4(base, (uint32_t)(r * a.q_tok_stride * 2) + (D >= 128 ? (lane & 1) * 128u : 0u),
+                 lds_addr(lds_sink));
+      }
+      if (wave == 0)
+        lds_dma4(a.block_table + (int64_t)nx.seq * a.bt_row_stride,
+                 4u * (uint32_t)(lane < a.max_blocks ? lane : a.max_blocks - 1), lds_addr(lds_sink));
+    }
 
     if (!wave_active) return;
-    const int row = wrow0 + r32;
     const float l = half_sum(l_run);
-    if (row >= n) return;
     const float inv = l > 0.f ? 1.f / l : 0.f;
-    // acc[dt][r] holds O[row][d = 32 dt + 8 (r/4) + 4 h + r%4].
-    u16* dst = a.out + ((tok0 + row) * a.num_heads + head) * (int64_t)D + 4 * h;
+    // The output tile (32 rows x D, the size of one K or V plane of a stage) goes through
+    // an LDS piece no wave reads after the tile's last barrier, so that every store
+    // covers whole rows.  After that barrier the waves read at most K of stage
+    // nsteps - 1 and V of stages nsteps - 2 and nsteps - 1 (slots mod NS); wave w takes
+    // the K plane of slot nsteps + w for w < NS - 1, else the V plane of slot
+    // nsteps + w - (NS - 1).  Chunk c (16 bytes) of row r sits at chunk c ^ (r % CPR).
+    u16* piece;
+    {
+      const int k = wave < NS - 1 ? wave : wave - (NS - 1);
+      const int sl = (nsteps + k) % NS;
+      piece = wave < NS - 1 ? lk[sl] : lv[sl];
+    }
+    // The lane number passes through an empty asm so that the offset arithmetic below
+    // stays here instead of being hoisted out of the tile loop (and kept live, in
+    // registers the ring needs).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int rr = ln & 31, hh = ln >> 5;
+    // acc[dt][i] holds O[row rr][d = 32 dt + 8 (i/4) + 4 hh + i%4]: chunk 4 dt + i/4, half hh.
 #pragma unroll
     for (int dt = 0; dt < DT; ++dt)
 #pragma unroll
       for (int b = 0; b < 4; ++b)
-        *reinterpret_cast<u32x2*>(dst + 32 * dt + 8 * b) =
+        *reinterpret_cast<u32x2*>(piece + rr * D + 8 * ((4 * dt + b) ^ (rr % CPR)) + 4 * hh) =
             u32x2{pack_bf16x2(acc[dt][4 * b] * inv, acc[dt][4 * b + 1] * inv),
                   pack_bf16x2(acc[dt][4 * b + 2] * inv, acc[dt][4 * b + 3] * inv)};
+    // Lane L reads back chunk L % CPR of row 64 / CPR * i + L / CPR (the wave's own writes:
+    // LDS accesses of one wave complete in order).
+    __builtin_amdgcn_wave_barrier();
+    constexpr int RPI = 64 / CPR;                     // rows per instruction
+    const int c = ln % CPR;
+    u32x4 ov[32 / RPI];
+#pragma unroll
+    for (int i = 0; i < 32 / RPI; ++i) {
+      const int r = RPI * i + ln / CPR;
+      ov[i] = *reinterpret_cast<const u32x4*>(piece + r * D + 8 * (c ^ (r % CPR)));
+    }
+    u16* dst = a.out + ((tok0 + wrow0 + ln / CPR) * a.num_heads + head) * (int64_t)D + 8 * c;
+    const int64_t rstride = (int64_t)RPI * a.num_heads * D;   // elements per RPI rows
+    if (wrow0 + 32 <= n) {
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i) *reinterpret_cast<u32x4*>(dst + i * rstride) = ov[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32 / RPI; ++i)
+        if (wrow0 + RPI * i + ln / CPR < n) *reinterpret_cast<u32x4*>(dst + i * rstride) = ov[i];
+    }
   };  // tile
 
   if (!a.persistent) {
-    tile(blockIdx.y, a.num_qtiles - 1 - (int)blockIdx.z, blockIdx.x / a.head_chunks,
-         blockIdx.x % a.head_chunks);
+    tile(resolve(blockIdx.y, a.num_qtiles - 1 - (int)blockIdx.z, blockIdx.x / a.head_chunks,
+                 blockIdx.x % a.head_chunks),
+         PrefTile{0, 0, 0, 0, 0, 0, 0}, [] {});
     return;
   }
 
@@ -570,27 +698,45 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   const int total = NQ > 0 ? s_off[0] + s_cnt[0] * KVC : 0;
   const int G = gridDim.x, w = blockIdx.x;
   int lvl = NQ - 1;
-  for (int r = 0; r * G < total; ++r) {
-    const int j = (r & 1) ? r * G + (G - 1 - w) : r * G + w;
-    if (j >= total) continue;
-    while (j >= s_off[lvl] + s_cnt[lvl] * KVC) --lvl;        // j only grows
-    const int i = j - s_off[lvl];
-    int rank = i / KVC;
-    const int c = i - rank * KVC;
-    int seq = -1;
-    for (int base = 0; base < S && seq < 0; base += 64) {
-      const int q = base + lane;
-      const uint64_t m = __builtin_amdgcn_ballot_w64(q < S && s_ntiles[q] > lvl);
-      const int pc = __builtin_popcountll(m);
-      if (rank < pc) {
-        uint64_t mm = m;
-        for (int k = 0; k < rank; ++k) mm &= mm - 1;       // drop the lowest `rank` bits
-        seq = base + __builtin_ctzll(mm);
-      } else {
-        rank -= pc;
+  int r = 0;
+  // The item of the next round that has one, resolved (false: none left).
+  auto next_item = [&](PrefTile& out) {
+    for (; r * G < total; ++r) {
+      const int j = (r & 1) ? r * G + (G - 1 - w) : r * G + w;
+      if (j >= total) continue;
+      while (j >= s_off[lvl] + s_cnt[lvl] * KVC) --lvl;      // j only grows
+      const int i = j - s_off[lvl];
+      int rank = i / KVC;
+      const int c = i - rank * KVC;
+      int seq = -1;
+      for (int base = 0; base < S && seq < 0; base += 64) {
+        const int q = base + lane;
+        const uint64_t m = __builtin_amdgcn_ballot_w64(q < S && s_ntiles[q] > lvl);
+        const int pc = __builtin_popcountll(m);
+        if (rank < pc) {
+          uint64_t mm = m;
+          for (int k = 0; k < rank; ++k) mm &= mm - 1;     // drop the lowest `rank` bits
+          seq = base + __builtin_ctzll(mm);
+        } else {
+          rank -= pc;
+        }
       }
+      out = resolve(seq, lvl, c / a.head_chunks, c % a.head_chunks);
+      ++r;
+      return true;
     }
-    tile(seq, lvl, c / a.head_chunks, c % a.head_chunks);
+    return false;
+  };
+  // One tile ahead: each tile resolves the next one while its own first loads are out.
+  PrefTile cur, nxt;
+  bool have = next_item(cur), more = false;
+  while (have) {
+    tile(cur, nxt, [&] {
+      more = next_item(nxt);
+      if (!more) nxt.n = 0;
+    });
+    cur = nxt;
+    have = more;
   }
 }
 
@@ -681,7 +827,7 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
   a.num_seqs = num_seqs;
   a.persistent = num_seqs <= kPrefListSeqs && qtiles <= kPrefListLevels &&
                  gx * (int64_t)num_seqs * qtiles < ((int64_t)1 << 31);
-  const void* fn = head_dim == 128 ? (const void*)varlen_prefill_kernel<128, 5>
+  const void* fn = head_dim == 128 ? (const void*)varlen_prefill_kernel<128, 6>
                                    : (const void*)varlen_prefill_kernel<64, 8>;
   dim3 grid((unsigned)gx, (unsigned)num_seqs, (unsigned)qtiles);
   if (a.persistent) {
@@ -691,7 +837,7 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
     grid = dim3((unsigned)(items < slots ? items : slots), 1, 1);
   }
   if (head_dim == 128)
-    hipLaunchKernelGGL((varlen_prefill_kernel<128, 5>), grid, dim3(64 * waves), 0, s, a);
+    hipLaunchKernelGGL((varlen_prefill_kernel<128, 6>), grid, dim3(64 * waves), 0, s, a);
   else
     hipLaunchKernelGGL((varlen_prefill_kernel<64, 8>), grid, dim3(64 * waves), 0, s, a);
   return check_launch();

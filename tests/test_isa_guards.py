@@ -35,5 +35,5 @@ def test_prefill_kernels_use_m0_only_for_direct_lds_loads(tmp_path):
             if not re.search(r"\bm0\b", l):
                 continue
             assert l.startswith("s_mov_b32 m0, s"), l
-            assert body[i + 1] == "s_nop 0" and body[i + 2].startswith("global_load_lds_dwordx4"), \
+            assert body[i + 1] == "s_nop 0" and re.match(r"global_load_lds_dword(x4)? ", body[i + 2]), \
                 body[i:i + 3]
