@@ -83,12 +83,13 @@ struct PrefillArgs {
   int persistent;     // 1: grid of resident workgroups walking the tile list
 };
 
-// One query tile, resolved one tile ahead by the persistent walk: rows
-// qtile * wg_rows .. of sequence seq (tokens tok0 .., n rows, ctx cached tokens before
-// them), kv head kvh, head chunk chunk.  n == 0: nothing to compute.
+// One query tile, looked up one tile ahead by the persistent walk: rows
+// qtile * wg_rows .. of sequence seq, kv head kvh, head chunk chunk, with the sequence's
+// cu_seqlens pair and context length as loaded (checked where they are used, so that
+// the look-up does not wait for the loads).  seq < 0: no tile.
 struct PrefTile {
-  int64_t tok0;
-  int seq, qtile, kvh, chunk, n, ctx;
+  int seq, qtile, kvh, chunk;
+  int tok0, tok1, ctx;
 };
 
 typedef __attribute__((ext_vector_type(16))) float f32x16;
@@ -185,18 +186,20 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   const int r32 = lane & 31, h = lane >> 5;
   const int wg_rows = kPrefRows * a.subtiles;
 
-  // Sequence bounds of a tile (scalar loads).  Rows past num_tokens are never touched,
-  // whatever cu_seqlens holds.
-  auto resolve = [&](int seq, int qtile, int kvh, int chunk) {
-    PrefTile t{0, seq, qtile, kvh, chunk, 0, 0};
-    const int64_t tok0 = a.cu_seqlens[seq];
-    int64_t tok1 = a.cu_seqlens[seq + 1];
-    if (tok1 > a.num_tokens) tok1 = a.num_tokens;
-    if (tok0 < 0 || tok1 <= tok0 || (int64_t)qtile * wg_rows >= tok1 - tok0) return t;
-    t.tok0 = tok0;
-    t.n = (int)(tok1 - tok0);
-    t.ctx = a.context_lens[seq] < 0 ? 0 : a.context_lens[seq];
-    return t;
+  auto look_up = [&](int seq, int qtile, int kvh, int chunk) {
+    return PrefTile{seq, qtile, kvh, chunk, a.cu_seqlens[seq], a.cu_seqlens[seq + 1],
+                    a.context_lens[seq]};
+  };
+  // A tile's first token, rows and cached tokens; false if it has no rows.  Rows past
+  // num_tokens are never touched, whatever cu_seqlens holds.
+  auto bounds = [&](const PrefTile& t, int64_t& tok0, int& n, int& ctx) {
+    if (t.seq < 0) return false;
+    tok0 = t.tok0;
+    const int64_t tok1 = t.tok1 < a.num_tokens ? (int64_t)t.tok1 : a.num_tokens;
+    if (tok0 < 0 || tok1 <= tok0 || (int64_t)t.qtile * wg_rows >= tok1 - tok0) return false;
+    n = (int)(tok1 - tok0);
+    ctx = t.ctx < 0 ? 0 : t.ctx;
+    return true;
   };
 
   // One query tile (see PrefTile).  Every wave of the workgroup runs it together (it has
@@ -204,12 +207,13 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   // (n == 0: none); it runs while the tile's first loads are in flight, and nx's Q rows
   // and table window are pulled into the L2 at the end of this tile.
   auto tile = [&](const PrefTile& t, const PrefTile& nx, auto&& ahead) {
-    if (t.n <= 0) {
+    int64_t tok0;
+    int n, ctx;
+    if (!bounds(t, tok0, n, ctx)) {
       ahead();
       return;
     }
-    const int seq = t.seq, kvh = t.kvh, n = t.n, ctx = t.ctx;
-    const int64_t tok0 = t.tok0;
+    const int seq = t.seq, kvh = t.kvh;
     const int hg = t.chunk * a.heads_per_wg + hw;                // head within the group
     const int head = kvh * a.group + hg;
     const int row0 = t.qtile * wg_rows;
@@ -569,12 +573,14 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     // L2, after the ring's last wait: direct loads into a scratch LDS word per lane that
     // nothing reads, retired by the next tile's first wait.  Lane l touches row l / 2,
     // 128-byte half l % 2 of the row's head slice.
-    if (nx.n > 0) {
+    int64_t ntok0;
+    int nn, nctx;
+    if (bounds(nx, ntok0, nn, nctx)) {
       const int nrow0 = nx.qtile * wg_rows + sub * kPrefRows;
       const int nhg = nx.chunk * a.heads_per_wg + hw;
-      if (nrow0 < nx.n && nhg < a.group && sub < a.subtiles) {
-        const int r = nrow0 + (lane >> 1) < nx.n ? lane >> 1 : 0;
-        const u16* base = a.q + (nx.tok0 + nrow0) * a.q_tok_stride +
+      if (nrow0 < nn && nhg < a.group && sub < a.subtiles) {
+        const int r = nrow0 + (lane >> 1) < nn ? lane >> 1 : 0;
+        const u16* base = a.q + (ntok0 + nrow0) * a.q_tok_stride +
                           (int64_t)(nx.kvh * a.group + nhg) * D;
         lds_dma4(base, (uint32_t)(r * a.q_tok_stride * 2) + (D >= 128 ? (lane & 1) * 128u : 0u),
                  lds_addr(lds_sink));
@@ -637,9 +643,9 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   };  // tile
 
   if (!a.persistent) {
-    tile(resolve(blockIdx.y, a.num_qtiles - 1 - (int)blockIdx.z, blockIdx.x / a.head_chunks,
+    tile(look_up(blockIdx.y, a.num_qtiles - 1 - (int)blockIdx.z, blockIdx.x / a.head_chunks,
                  blockIdx.x % a.head_chunks),
-         PrefTile{0, 0, 0, 0, 0, 0, 0}, [] {});
+         PrefTile{-1, 0, 0, 0, 0, 0, 0}, [] {});
     return;
   }
 
@@ -704,24 +710,36 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     for (; r * G < total; ++r) {
       const int j = (r & 1) ? r * G + (G - 1 - w) : r * G + w;
       if (j >= total) continue;
-      while (j >= s_off[lvl] + s_cnt[lvl] * KVC) --lvl;      // j only grows
+      // Level of item j (j only grows): the highest t <= lvl with
+      // j < s_off[t] + s_cnt[t] * KVC (the items in levels >= t), 64 levels per look.
+      for (;;) {
+        const int t = lvl - lane;
+        const uint64_t m = __builtin_amdgcn_ballot_w64(t >= 0 && j < s_off[t] + s_cnt[t] * KVC);
+        if (m != 0) {
+          lvl -= __builtin_ctzll(m);
+          break;
+        }
+        lvl -= 64;
+      }
       const int i = j - s_off[lvl];
       int rank = i / KVC;
       const int c = i - rank * KVC;
       int seq = -1;
       for (int base = 0; base < S && seq < 0; base += 64) {
         const int q = base + lane;
-        const uint64_t m = __builtin_amdgcn_ballot_w64(q < S && s_ntiles[q] > lvl);
+        const bool has = q < S && s_ntiles[q] > lvl;
+        const uint64_t m = __builtin_amdgcn_ballot_w64(has);
         const int pc = __builtin_popcountll(m);
         if (rank < pc) {
-          uint64_t mm = m;
-          for (int k = 0; k < rank; ++k) mm &= mm - 1;     // drop the lowest `rank` bits
-          seq = base + __builtin_ctzll(mm);
+          // the lane whose bit is set with `rank` set bits below it
+          const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
+                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
+          seq = base + __builtin_ctzll(__builtin_amdgcn_ballot_w64(has && below == rank));
         } else {
           rank -= pc;
         }
       }
-      out = resolve(seq, lvl, c / a.head_chunks, c % a.head_chunks);
+      out = look_up(seq, lvl, c / a.head_chunks, c % a.head_chunks);
       ++r;
       return true;
     }
@@ -733,7 +751,7 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   while (have) {
     tile(cur, nxt, [&] {
       more = next_item(nxt);
-      if (!more) nxt.n = 0;
+      if (!more) nxt.seq = -1;
     });
     cur = nxt;
     have = more;
