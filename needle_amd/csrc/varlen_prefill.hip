@@ -465,30 +465,13 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       }
     };
 
-    // One step: QK(step + 1) and the softmax + PV of step, after the trip's barrier if
-    // `mode` has one.  Masking (steps that reach past a wave's first query position, the
-    // tail, invalid blocks) and the rare rescale are the only other branches.  QK of a
-    // step past the last one reads a stale slot; its scores are never used.
-    auto iteration = [&](int step, int stage, f32x16& st_cur, f32x16& st_next, int mode) {
-      const int nstage = stage + 1 == NS ? 0 : stage + 1;
-      int need = 0;
-      if (mode != kNone) need = sync(step, mode);
-      // The LDS reads (K of step + 1, V of this step) and the QK MFMAs of step + 1 depend on
-      // nothing below, so they go out first: the matrix core runs while the ring upkeep,
-      // the row max, the growth check and the exponentials of this step run.  The upkeep
-      // writes only slots no wave reads before the next barrier: those of steps before
-      // this one, and V of step `need`, read after it.
-      u32x4 ka[KS];
-      bf16x8 vop[2 * DT];
-      k_reads(nstage, ka);
-      v_reads(stage, vop);
-      st_next = qk(ka);
-      if (mode != kNone) upkeep(step, stage, need, mode);
+    // Softmax and PV of one step whose scores are st (may_mask false: the caller knows
+    // the step needs no mask).
+    auto finish = [&](int step, int stage, f32x16 st, const bf16x8* vop, bool may_mask) {
       const int kv0 = step * kPrefKeys;
       const bool masked = kv0 + kPrefKeys - 1 > qpos_min || kv0 + kPrefKeys > kv_end ||
                           ((badbits >> (2 * stage)) & 3u) != 0;
-      f32x16 st = st_cur;
-      if (masked) {
+      if (may_mask && masked) {
         const bool bad0 = (badbits >> (2 * stage)) & 1u;
         const bool bad1 = (badbits >> (2 * stage + 1)) & 1u;
 #pragma unroll
@@ -544,6 +527,28 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       pv(vop, pw);
     };
 
+    // One step: QK(step + 1) and the softmax + PV of step, after the trip's barrier if
+    // `mode` has one.  Masking (steps that reach past a wave's first query position, the
+    // tail, invalid blocks) and the rare rescale are the only other branches.  QK of a
+    // step past the last one reads a stale slot; its scores are never used.
+    auto iteration = [&](int step, int stage, f32x16& st_cur, f32x16& st_next, int mode) {
+      const int nstage = stage + 1 == NS ? 0 : stage + 1;
+      int need = 0;
+      if (mode != kNone) need = sync(step, mode);
+      // The LDS reads (K of step + 1, V of this step) and the QK MFMAs of step + 1 depend on
+      // nothing below, so they go out first: the matrix core runs while the ring upkeep,
+      // the row max, the growth check and the exponentials of this step run.  The upkeep
+      // writes only slots no wave reads before the next barrier: those of steps before
+      // this one, and V of step `need`, read after it.
+      u32x4 ka[KS];
+      bf16x8 vop[2 * DT];
+      k_reads(nstage, ka);
+      v_reads(stage, vop);
+      st_next = qk(ka);
+      if (mode != kNone) upkeep(step, stage, need, mode);
+      finish(step, stage, st_cur, vop, true);
+    };
+
     // Ring: steps 0 .. NS-3 in flight at the start.  The first barrier retires every
     // wave's reads of the previous tile (persistent launch) before the slots are refilled.
     lds_barrier();
@@ -560,6 +565,53 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       st0 = qk(ka);
     }
     int step = 0, stage = 0;
+
+    // Steady trips: both steps' keys lie wholly below every wave's first query row (no
+    // mask), all NS - 1 steps ahead exist (so the load wait is a constant and nothing
+    // needs clearing), their table columns exist, and no block id in flight is invalid.
+    // Same ring protocol as a paired trip below, without its bookkeeping.
+    {
+      const int free_steps = (ctx + row0 + 1) / kPrefKeys;   // steps below row0's first query
+      int lim = free_steps - 1;
+      if (nsteps - NS + 1 < lim) lim = nsteps - NS + 1;
+      if ((a.max_blocks - 2) / 2 - NS + 2 < lim) lim = (a.max_blocks - 2) / 2 - NS + 2;
+      // Issues step x into slot sl (columns 2x, 2x + 1 exist); the general path once a
+      // table window holds an invalid id.
+      auto stage_fast = [&](int x, int sl) {
+        const int c0 = 2 * x;
+        if (c0 >= win0 + 64 || win_bad) {
+          stage_in(x, sl);
+          return;
+        }
+        if (!loader) return;
+        const uint32_t b = (uint32_t)__builtin_amdgcn_readlane(btw, c0 + ld_blk - win0);
+        const u16* base = ld_head + (int64_t)b * blk_stride;
+        const uint32_t lds = ld_lds + (uint32_t)sl * (kPrefKeys * D * 2);
+#pragma unroll
+        for (int e = 0; e < IPW; ++e)
+          lds_dma16(base, ld_off[e], lds + 1024 * e);
+      };
+      for (; step < lim && badbits == 0; step += 2) {
+        const int stage1 = stage + 1 == NS ? 0 : stage + 1;
+        const int stage2 = stage1 + 1 == NS ? 0 : stage1 + 1;
+        if (loader) vm_wait<(NS - 5) * IPW>();   // steps step + 3 .. step + NS - 3 stay out
+        lds_barrier();
+        u32x4 ka[KS];
+        bf16x8 vop[2 * DT];
+        k_reads(stage1, ka);
+        v_reads(stage, vop);
+        st1 = qk(ka);
+        stage_fast(step + NS - 2, slot_after(stage, NS - 2));
+        stage_fast(step + NS - 1, slot_after(stage, NS - 1));
+        finish(step, stage, st0, vop, false);
+        k_reads(stage2, ka);
+        v_reads(stage1, vop);
+        st0 = qk(ka);
+        finish(step + 1, stage1, st1, vop, false);
+        stage = stage2;
+      }
+    }
+
     for (; step + 2 <= nsteps; step += 2) {
       const int stage1 = stage + 1 == NS ? 0 : stage + 1;
       const bool pair = !needs_vzero(step + 1, stage1);
