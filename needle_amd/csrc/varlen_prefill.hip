@@ -566,20 +566,19 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     }
     int step = 0, stage = 0;
 
-    // Steady trips: both steps' keys lie wholly below every wave's first query row (no
-    // mask), all NS - 1 steps ahead exist (so the load wait is a constant and nothing
-    // needs clearing), their table columns exist, and no block id in flight is invalid.
-    // Same ring protocol as a paired trip below, without its bookkeeping.
+    // Unmasked trips: both steps' keys lie wholly below every wave's first query row (no
+    // mask, full steps) and no block id in flight is invalid.  The ring protocol of a
+    // paired trip below, with only the bookkeeping such a trip needs: a constant load
+    // wait while the ring is in full flow, staging of the steps that exist, clearing of
+    // step + 2 (the last step can be partial).
     {
-      const int free_steps = (ctx + row0 + 1) / kPrefKeys;   // steps below row0's first query
-      int lim = free_steps - 1;
-      if (nsteps - NS + 1 < lim) lim = nsteps - NS + 1;
-      if ((a.max_blocks - 2) / 2 - NS + 2 < lim) lim = (a.max_blocks - 2) / 2 - NS + 2;
-      // Issues step x into slot sl (columns 2x, 2x + 1 exist); the general path once a
-      // table window holds an invalid id.
+      const int lim = (ctx + row0 + 1) / kPrefKeys - 1;   // t + 1 < steps below row0's first query
+      // Issues step x into slot sl if it exists; the general path for a new table window,
+      // a window with an invalid id, or a table row too short for the step.
       auto stage_fast = [&](int x, int sl) {
+        if (x >= nsteps) return;
         const int c0 = 2 * x;
-        if (c0 >= win0 + 64 || win_bad) {
+        if (c0 >= win0 + 64 || win_bad || c0 + 1 >= a.max_blocks) {
           stage_in(x, sl);
           return;
         }
@@ -594,7 +593,16 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       for (; step < lim && badbits == 0; step += 2) {
         const int stage1 = stage + 1 == NS ? 0 : stage + 1;
         const int stage2 = stage1 + 1 == NS ? 0 : stage1 + 1;
-        if (loader) vm_wait<(NS - 5) * IPW>();   // steps step + 3 .. step + NS - 3 stay out
+        // Loads of steps up to step + 2 (the last one at most) landed: steps issued after
+        // it stay out, NS - 5 of them while the ring is in full flow.
+        if (loader) {
+          if (step + NS - 3 <= nsteps - 1) {
+            vm_wait<(NS - 5) * IPW>();
+          } else {
+            const int need = step + 2 < nsteps - 1 ? step + 2 : nsteps - 1;
+            wait_loads(nsteps - 1 - need);
+          }
+        }
         lds_barrier();
         u32x4 ka[KS];
         bf16x8 vop[2 * DT];
@@ -603,6 +611,7 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
         st1 = qk(ka);
         stage_fast(step + NS - 2, slot_after(stage, NS - 2));
         stage_fast(step + NS - 1, slot_after(stage, NS - 1));
+        if (step + 2 < nsteps && needs_vzero(step + 2, stage2)) zero_v(step + 2, stage2);
         finish(step, stage, st0, vop, false);
         k_reads(stage2, ka);
         v_reads(stage1, vop);
