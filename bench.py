@@ -203,7 +203,6 @@ def extra_measurements(torch, ops, wl, reps):
         ops.varlen_prefill(c3.q, c3.kv_cache, c3.block_table, c3.cu_seqlens, c3.context_lens,
                            c3.max_seqlen, s3.scale, s3.num_heads, s3.num_kv_heads, s3.head_dim)
     app3()
-    warm(torch, att3, 1.5)
 
     def app3_x10():
         for _ in range(10):
@@ -211,14 +210,38 @@ def extra_measurements(torch, ops, wl, reps):
     g3 = capture(torch, app3_x10)   # ~13 us launches: replayed, so host time stays out
     ms_a = time_region(torch, g3.replay, reps) / 10
     del g3
-    ms_p = time_region(torch, att3, reps)
     t3 = sum(c3.new_lens)
     ab = wl.append_bytes(s3, t3, c3.num_seqs, varlen=True)
+
+    # The same append fused with RoPE on q and k (rotated q written to a separate buffer).
+    gen = torch.Generator(device=dev).manual_seed(7)
+    cos3 = torch.randn(t3, s3.head_dim, device=dev, generator=gen).to(torch.bfloat16)
+    sin3 = torch.randn(t3, s3.head_dim, device=dev, generator=gen).to(torch.bfloat16)
+    qrot3 = torch.empty_like(c3.q)
+
+    def rope3_x10():
+        for _ in range(10):
+            ops.rope_kv_append(c3.q, c3.k, c3.v, cos3, sin3, c3.kv_cache, c3.block_table,
+                               c3.context_lens, cu_seqlens=c3.cu_seqlens, out=qrot3)
+    rope3_x10()
+    g3r = capture(torch, rope3_x10)
+    ms_r = time_region(torch, g3r.replay, reps) / 10
+    del g3r
+    # q read and rotated q written, cos/sin read, plus the append's bytes
+    rb = 2 * t3 * s3.num_heads * s3.head_dim * 2 + 2 * t3 * s3.head_dim * 2 + ab
+    app3()   # the cache holds k again (the rotated rows only changed its values)
+    # The prefill is compute-bound: its clock ramps over ~1 s of load, so it is timed right
+    # after 1.5 s of warm-up launches.
+    warm(torch, att3, 1.5)
+    ms_p = time_region(torch, att3, reps)
     fl = wl.prefill_flops(s3, c3.new_lens)
     res["qwen2_7b_prefill"] = {
         "tokens": t3, "append_us": round(ms_a * 1e3, 2),
         "append_gbs": round(ab / ms_a / 1e6, 1),
         "append_frac_of_hbm_peak": round(ab / ms_a / 1e6 / HBM_PEAK_GBS, 4),
+        "rope_append_us": round(ms_r * 1e3, 2),
+        "rope_append_gbs": round(rb / ms_r / 1e6, 1),
+        "rope_append_frac_of_hbm_peak": round(rb / ms_r / 1e6 / HBM_PEAK_GBS, 4),
         "attention_us": round(ms_p * 1e3, 2),
         "attention_tflops": round(fl / ms_p / 1e9, 1),
         "attention_frac_of_mfma_peak": round(fl / ms_p / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
