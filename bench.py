@@ -54,6 +54,9 @@ def parse_args():
     p.add_argument("--no-e2e", action="store_true", help="skip the end-to-end engine run")
     p.add_argument("--e2e-seconds", type=float, default=120.0,
                    help="time limit of the end-to-end run (it finishes in about 30 s)")
+    p.add_argument("--ceilings", action="store_true",
+                   help="measure what library kernels reach on this GPU (a 4 GiB read-only "
+                        "reduction, a 4 GiB copy, an 8192^3 bf16 GEMM) and exit")
     p.add_argument("--profile", nargs="?", const="decode", choices=["decode", "prefill"],
                    help="counter-collection driver, no timing output: --steps steps of the "
                         "decode workload (decode) or --steps rounds of the Qwen2-7B varlen "
@@ -269,6 +272,28 @@ def extra_measurements(torch, ops, wl, reps):
     return res
 
 
+def ceilings(torch):
+    """Practical ceilings from library kernels, to read the roofline fractions against."""
+    dev = torch.device("cuda:0")
+    n = 2 << 30                                   # 4 GiB of bf16
+    x = torch.ones(n, dtype=torch.bfloat16, device=dev)
+    y = torch.empty_like(x)
+    k = 8192
+    a = torch.randn(k, k, dtype=torch.bfloat16, device=dev)
+    b = torch.randn(k, k, dtype=torch.bfloat16, device=dev)
+    res = {}
+    for name, fn, work, unit in (
+            ("read_reduction_gbs", lambda: x.sum(dtype=torch.float32), 2 * n, "GB"),
+            ("copy_read_plus_write_gbs", lambda: y.copy_(x), 4 * n, "GB"),
+            ("gemm_bf16_8192_tflops", lambda: a @ b, 2 * k ** 3, "TFLOP")):
+        warm(torch, fn, 1.0)
+        ms = time_region(torch, fn, 10)
+        res[name] = round(work / (ms / 1e3) / (1e9 if unit == "GB" else 1e12), 1)
+    res["hbm_peak_gbs"] = HBM_PEAK_GBS
+    res["mfma_bf16_peak_tflops"] = MFMA_BF16_PEAK_TFLOPS
+    return res
+
+
 def cpu_baseline(torch, wl, shape, ctx, budget_s):
     """The reference torch path on the CPU (append + _decode_pytorch), one layer, repeated."""
     from oracle import paged_ref
@@ -305,6 +330,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         sys.exit(1)
+    if args.ceilings:
+        print(json.dumps({"ceilings": ceilings(torch)}), flush=True)
+        return
     dev = torch.device("cuda:0")
     (shape, ctx, tables, num_blocks, bt, ctx_t, pools, qs, ks, vs,
      outs) = build_workload(torch, wl, dev)
