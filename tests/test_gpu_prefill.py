@@ -149,3 +149,89 @@ def test_invalid_block_ids_are_masked():
                 pr = np.exp(sc - sc.max())
                 want[t, h] = pr @ vr / pr.sum()
     assert_close(got, want)
+
+
+def masked_prefill_fp64(case, bt, pool):
+    """fp64 causal attention reading every position of pool (after the append) through bt;
+    keys in a block whose id is outside [0, num_blocks) are dropped (a row with no key left
+    is zero).  Vectorised per (sequence, kv head), for the longer and more numerous prompts
+    below; it agrees with closed_form.prefill_fp64 to 1e-15 where both apply."""
+    s = case.shape
+    pool = pool.double().numpy()
+    nb = pool.shape[1]
+    qn = case.q.double().numpy()
+    btl = bt.tolist()
+    cu = case.cu_seqlens.tolist()
+    ctx = case.context_lens.tolist()
+    out = np.zeros(qn.shape)
+    for i in range(len(cu) - 1):
+        n, c = cu[i + 1] - cu[i], ctx[i]
+        if n == 0:
+            continue
+        w = len(btl[i])
+        pos = np.arange(c + n)
+        ids = np.array([btl[i][min(p // 16, w - 1)] for p in range(c + n)])
+        valid = (ids >= 0) & (ids < nb)
+        safe = np.where(valid, ids, 0)
+        mask = (pos[None, :] <= (c + np.arange(n))[:, None]) & valid[None, :]
+        for kvh in range(s.num_kv_heads):
+            kr = pool[0, safe, kvh, pos % 16]
+            vr = pool[1, safe, kvh, pos % 16]
+            for h in range(kvh * s.group, (kvh + 1) * s.group):
+                sc = qn[cu[i]:cu[i + 1], h] @ kr.T * s.scale
+                sc = np.where(mask, sc, -np.inf)
+                mx = sc.max(axis=1, keepdims=True)
+                pr = np.where(mask, np.exp(sc - np.where(np.isfinite(mx), mx, 0.0)), 0.0)
+                den = pr.sum(axis=1, keepdims=True)
+                out[cu[i]:cu[i + 1], h] = np.where(den > 0, (pr @ vr) / np.where(den > 0, den, 1), 0)
+    return out
+
+
+@pytest.mark.parametrize("shape", [wl.QWEN2_7B, wl.LLAMA3_8B])
+def test_long_prompts_after_cached_prefixes_vs_fp64(shape):
+    """Long cached prefixes (not multiples of the 32-key step) in front of long prompts: the
+    unmasked steady-state trips start at the context, cross several 64-block table windows
+    and hand over to the masked steps at each tile's diagonal."""
+    lens, ctx = [300, 77, 33, 129], [1000, 2100, 31, 0]
+    case = wl.prefill_case(shape, lens, seed=306, ctx_lens=ctx)
+    got, pool = run_gpu(case, max_ctx=max(ctx))
+    _, want_pool = oracle(case)
+    assert torch.equal(pool.view(torch.int16), want_pool.view(torch.int16))
+    assert_close(got, masked_prefill_fp64(case, case.block_table, pool))
+
+
+def test_invalid_block_deep_in_long_prompts():
+    """An invalid id far into a long prompt (after a table-window refill) ends the steady-state
+    trips; one early in another prompt keeps them from starting.  Keys in those blocks drop
+    out; every other key is attended."""
+    shape = wl.QWEN2_7B
+    case = wl.prefill_case(shape, [1500, 600, 1100], seed=307)
+    nb = case.kv_cache.shape[1]
+    bt = case.block_table.clone()
+    bt[0, 70] = -5          # positions 1120..1135 (table window 1)
+    bt[1, 5] = nb + 3       # positions 80..95
+    bt[2, 64] = -1          # positions 1024..1039: the first block of window 1
+    case.block_table = bt
+    got, pool = run_gpu(case)
+    assert_close(got, masked_prefill_fp64(case, bt, pool))
+
+
+@pytest.mark.parametrize("shape", [wl.QWEN2_7B, wl.QWEN2_05B])
+def test_many_prompts_tile_walk(shape):
+    """150 prompts: the persistent walk's sequence search spans three 64-lane chunks."""
+    lens = np.random.default_rng(308).integers(1, 120, size=150).tolist()
+    case = wl.prefill_case(shape, lens, seed=308)
+    got, pool = run_gpu(case)
+    assert_close(got, masked_prefill_fp64(case, case.block_table, pool))
+
+
+def test_one_workgroup_per_tile_beyond_the_tile_list():
+    """More than 8192 prompts: the tile list would not fit in LDS, so the kernel launches one
+    workgroup per tile instead of the persistent walk."""
+    shape = wl.HeadShape(8, 1, 64)
+    lens = np.random.default_rng(309).integers(1, 4, size=8200).tolist()
+    case = wl.prefill_case(shape, lens, seed=309)
+    got, pool = run_gpu(case)
+    _, want_pool = oracle(case)
+    assert torch.equal(pool.view(torch.int16), want_pool.view(torch.int16))
+    assert_close(got, masked_prefill_fp64(case, case.block_table, pool))
