@@ -350,16 +350,26 @@ def main():
     def append_layer(l):
         ops.kv_append(ks[l], vs[l], pools[l], bt, ctx_t)
 
-    def step():
+    def fused_layer(l):
+        # the reference's _decode (attention.py:141-159): append + attention, one launch
+        ops.paged_decode(qs[l], pools[l], bt, ctx_t, sc, h, hkv, d,
+                         partition_tokens=args.partition, out=outs[l], workspace=ws,
+                         new_k=ks[l], new_v=vs[l])
+
+    def step_separate():
         for l in range(LAYERS):
             append_layer(l)
             decode_layer(l)
 
+    def step():
+        for l in range(LAYERS):
+            fused_layer(l)
+
     if args.profile:
         info = {"profile": args.profile, "profile_steps": args.steps}
         if args.profile == "decode":
-            for _ in range(args.steps):
-                step()
+            for _ in range(args.steps):   # separate launches: the counters per kernel
+                step_separate()
             info.update(layers=LAYERS,
                         decode_algorithmic_bytes_per_launch=wl.decode_bytes(shape, ctx, width))
         else:
@@ -397,6 +407,9 @@ def main():
     # its decode steps (host launch overhead out of the timed region).
     g_step = capture(torch, step)
     ms_step = time_region(torch, g_step.replay, args.steps)
+    g_sep = capture(torch, step_separate)
+    ms_step_separate = time_region(torch, g_sep.replay, args.steps)
+    del g_sep
 
     # per-op timings over the same rotating pools, each a graph of its 32 launches
     def decode_all():
@@ -427,6 +440,7 @@ def main():
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "ms_per_step_eager": round(ms_step_eager, 4),
+        "ms_per_step_separate_launches": round(ms_step_separate, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -435,7 +449,8 @@ def main():
         "config": {
             "workload": "Llama-3-8B layer decode (32 layers): 32/8 heads, head_dim 128, "
                         "block_size 16, batch 64, context U[512,4096], bf16, random "
-                        "non-contiguous block tables, append + paged decode per layer",
+                        "non-contiguous block tables, append + paged decode per layer "
+                        "(one fused launch + merge)",
             "layers": LAYERS, "batch": len(ctx), "context_tokens": sum(ctx),
             "num_blocks_per_layer": num_blocks, "partition_tokens": args.partition or "auto",
             "decode_split": "per-sequence workgroups" if ws_bytes <= 256 else "stream split",

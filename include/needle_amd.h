@@ -1,7 +1,7 @@
 /*
  * needle_amd.h -- C ABI of the MI355X (gfx950) paged-KV hot path.
  *
- * Three operations replace the torch statement sequences of Needle's
+ * These operations replace the torch statement sequences of Needle's
  * needle/layers/attention.py:
  *
  *   ndl_kv_append       scatter new K/V rows into the block pool
@@ -11,6 +11,8 @@
  *   ndl_paged_decode    one-query-per-sequence attention over block_table
  *                       (_decode_pytorch :291-310, dispatched from _decode :156-159;
  *                        also covers the FlashInfer wrapper :161-197)
+ *   ndl_paged_decode_append  the decode append and that attention in one launch
+ *                       (_decode :141-159)
  *   ndl_varlen_prefill  causal attention of packed varlen prompts, reading K/V
  *                       back through block_table
  *                       (_prefill_pytorch :120-134; FlashInfer path :109-118)
@@ -154,6 +156,32 @@ int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
                      int num_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
                      float scale, int partition_tokens,
                      void* workspace, size_t workspace_bytes, ndl_stream_t stream);
+
+/*
+ * The decode step of Attention._decode in one launch: the append of the step's new
+ * k/v rows and the paged attention that reads them.
+ *
+ * Replaces: needle/layers/attention.py:141-159 (the append :141-154, then the
+ *           attention :156-159, _decode_pytorch :291-310).
+ *
+ * Same cache bytes and the same out as ndl_kv_append (cu_seqlens NULL: k/v row i is
+ * sequence i's token at position context_lens[i]) followed by ndl_paged_decode with
+ * the same arguments: the wave that attends a sequence's last block writes the new row
+ * there and attends it in place of the row it read.  k, v: [num_seqs][num_kv_heads]
+ * [head_dim], token strides k_tok_stride / v_tok_stride (multiples of 8, 16-byte
+ * aligned rows).  Requires that no block is attended by two sequences (BlockAllocator
+ * hands every block to one sequence, block_allocator.py:37-56); the workspace is the
+ * one ndl_paged_decode_workspace_bytes sizes.
+ */
+int ndl_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
+                            const void* k, int64_t k_tok_stride,
+                            const void* v, int64_t v_tok_stride,
+                            void* kv_cache, int64_t num_blocks,
+                            const int32_t* block_table, int64_t bt_row_stride,
+                            int max_blocks_per_seq, const int32_t* context_lens, int num_seqs,
+                            int num_heads, int num_kv_heads, int head_dim, int block_size,
+                            int dtype, float scale, int partition_tokens,
+                            void* workspace, size_t workspace_bytes, ndl_stream_t stream);
 
 /*
  * Varlen causal prefill attention over the paged cache.

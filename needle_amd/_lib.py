@@ -27,6 +27,7 @@ EXPORTED_SYMBOLS = (
     "ndl_rope_kv_append",
     "ndl_paged_decode_workspace_bytes",
     "ndl_paged_decode",
+    "ndl_paged_decode_append",
     "ndl_varlen_prefill",
 )
 
@@ -56,6 +57,16 @@ _SIGNATURES = {
     "ndl_paged_decode_workspace_bytes": (_c_sz, [_c_i32] * 7),
     "ndl_paged_decode": (_c_i32, [
         _c_p, _c_p, _c_i64,                             # out, q, q stride
+        _c_p, _c_i64,                                   # cache, NB
+        _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
+        _c_p, _c_i32,                                   # ctx, B
+        _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # H, Hkv, D, bs, dtype
+        _c_f32, _c_i32,                                 # scale, partition
+        _c_p, _c_sz, _c_p,                              # workspace, bytes, stream
+    ]),
+    "ndl_paged_decode_append": (_c_i32, [
+        _c_p, _c_p, _c_i64,                             # out, q, q stride
+        _c_p, _c_i64, _c_p, _c_i64,                     # k, k stride, v, v stride
         _c_p, _c_i64,                                   # cache, NB
         _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
         _c_p, _c_i32,                                   # ctx, B

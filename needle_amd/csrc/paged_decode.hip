@@ -85,6 +85,11 @@ struct DecodeArgs {
   int nseg;       // segment slots per kv head: waves per kv head + num_seqs
   float* ws_ml;   // [kv head][segment][group head][2] = (m, l)
   float* ws_acc;  // [kv head][segment][group head][D]
+  // Fused append (null: none): the step's new k/v rows, [seq][kv head][D] with these token
+  // strides, written into the cache and attended in the same pass.
+  const u16* k_new;
+  const u16* v_new;
+  int64_t k_new_stride, v_new_stride;
 };
 
 __device__ __forceinline__ int64_t attended_len(const DecodeArgs& a, int seq) {
@@ -152,7 +157,7 @@ __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
 // NW == 1: one wave per workgroup, wave s of a kv head takes stream tiles s*C .. s*C + C.
 // NW > 1: one workgroup per (kv head, sequence); wave w takes tiles w*C .. w*C + C of
 // the sequence (C = ceil(n / NW)) and the waves combine through LDS.
-template <int D, int NBUF, int NW>
+template <int D, int NBUF, int NW, bool APP>
 __global__ __launch_bounds__(64 * NW) void paged_decode_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;   // k-steps of the QK^T MFMA
   constexpr int DPL = D / 16;  // head_dim elements per lane per V row
@@ -239,6 +244,22 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_kernel(DecodeArgs a) {
     }
     const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
 
+    // Fused append (attention.py:141-154 before :156-159): the new token of the step sits
+    // at position context_lens[seq], row context_lens[seq] % 16 of the sequence's last tile
+    // (the append's column min(p / 16, W - 1) is the last attended tile, also when the
+    // table row clamps).  The wave that owns that tile writes the row into the cache and
+    // uses it in place of the row it loaded; no other wave reads the tile.  Each lane loads
+    // the pieces of the new rows it holds in the tile layouts: chunk k_chunk of K, head_dim
+    // DPL*c .. of V.
+    const bool app = APP && lt1 == n_tiles;   // wave-uniform
+    const int r_new = app ? a.context_lens[seq] & 15 : 0;
+    u32x4 k_app = {0u, 0u, 0u, 0u};
+    VT v_app = {};
+    if (app) {
+      k_app = ld16(a.k_new + (int64_t)seq * a.k_new_stride + (int64_t)kvh * D + 8 * k_chunk);
+      v_app = load_vrow<D>(a.v_new + (int64_t)seq * a.v_new_stride + (int64_t)kvh * D + DPL * c);
+    }
+
     f32x4 acc[DPL];
 #pragma unroll
     for (int b = 0; b < DPL; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -262,6 +283,24 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_kernel(DecodeArgs a) {
       };
 
       auto compute_tile = [&](int it, Tile& t) {
+        if (app && w0 + it == n_tiles - 1 && !t.bad) {   // the appended token's tile
+          const int64_t blk = __builtin_amdgcn_readlane(bt_lane, it);
+          u16* const kb = const_cast<u16*>(a.kplane) + blk * blk_stride + head_off + r_new * D;
+          u16* const vb = const_cast<u16*>(a.vplane) + blk * blk_stride + head_off + r_new * D;
+#pragma unroll
+          for (int s = 0; s < KS; ++s)
+            if (RPI * s + k_row == r_new) t.k[s] = k_app;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (4 * j + i == r_new) t.v[i] = v_app;
+          if (k_row == r_new % RPI) st16(kb + 8 * k_chunk, k_app);
+          if (j == (r_new >> 2)) {
+            if constexpr (D == 128)
+              st16(vb + DPL * c, v_app);
+            else
+              *reinterpret_cast<VT*>(vb + DPL * c) = v_app;
+          }
+        }
         __builtin_amdgcn_wave_barrier();  // previous block's LDS reads are issued first
 #pragma unroll
         for (int s = 0; s < KS; ++s) {
@@ -574,10 +613,15 @@ inline int64_t decode_resident_waves(const void* fn, int block = 64) {
   return waves;
 }
 
-template <int D> const void* decode_kernel_fn(int depth) {
-  return depth == 2 ? (const void*)paged_decode_kernel<D, 2, 1>
-                    : depth == 4 ? (const void*)paged_decode_kernel<D, 4, 1>
-                                 : (const void*)paged_decode_kernel<D, 3, 1>;
+// APP: with the fused append (a separate instantiation, so that the attention-only kernel
+// carries none of its registers).
+template <int D, bool APP = false> const void* decode_kernel_fn(int depth) {
+  return depth == 2 ? (const void*)paged_decode_kernel<D, 2, 1, APP>
+                    : depth == 4 ? (const void*)paged_decode_kernel<D, 4, 1, APP>
+                                 : (const void*)paged_decode_kernel<D, 3, 1, APP>;
+}
+template <int D, bool APP = false> const void* seq_split_kernel_fn() {
+  return (const void*)paged_decode_kernel<D, 2, seq_split_waves<D>(), APP>;
 }
 
 struct DecodeLayout {
@@ -607,9 +651,7 @@ inline int decode_layout(int num_seqs, int num_heads, int num_kv_heads, int head
     return NDL_ERR_INVALID_ARG;
   } else if (partition_tokens == 0) {
     int64_t resident = decode_resident_waves(
-        head_dim == 128 ? (const void*)paged_decode_kernel<128, 2, seq_split_waves<128>()>
-                        : (const void*)paged_decode_kernel<64, 2, seq_split_waves<64>()>,
-        64 * nw);
+        head_dim == 128 ? seq_split_kernel_fn<128>() : seq_split_kernel_fn<64>(), 64 * nw);
     if (resident <= 0) resident = 2048;
     if ((int64_t)num_kv_heads * num_seqs * nw <= resident &&
         (max_blocks + nw - 1) / nw <= kSeqSplitMaxTiles)
@@ -661,14 +703,15 @@ extern "C" size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, 
   return lay.bytes;
 }
 
-extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
-                                const void* kv_cache, int64_t num_blocks,
-                                const int32_t* block_table, int64_t bt_row_stride,
-                                int max_blocks_per_seq, const int32_t* context_lens, int num_seqs,
-                                int num_heads, int num_kv_heads, int head_dim, int block_size,
-                                int dtype, float scale, int partition_tokens, void* workspace,
-                                size_t workspace_bytes, ndl_stream_t stream) {
-  using namespace ndl;
+namespace ndl {
+
+static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const void* kv_cache,
+                         int64_t num_blocks, const int32_t* block_table, int64_t bt_row_stride,
+                         int max_blocks_per_seq, const int32_t* context_lens, int num_seqs,
+                         int num_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
+                         float scale, int partition_tokens, void* workspace,
+                         size_t workspace_bytes, const void* k_new, int64_t k_new_stride,
+                         const void* v_new, int64_t v_new_stride, ndl_stream_t stream) {
   if (dtype != NDL_DTYPE_BF16) return NDL_ERR_UNSUPPORTED;
   if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -719,34 +762,32 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
   a.nseg = (int)lay.nseg;
   a.ws_ml = (float*)workspace;
   a.ws_acc = (float*)((char*)workspace + lay.ml_bytes);
+  a.k_new = (const u16*)k_new;
+  a.v_new = (const u16*)v_new;
+  a.k_new_stride = k_new_stride;
+  a.v_new_stride = v_new_stride;
 
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)grid_waves);
+  const bool app = k_new != nullptr;
+  void* args[] = {&a};
   if (lay.seq_split) {  // one workgroup per (kv head, sequence), kv head fastest
-    const dim3 block(64 * lay.seq_split);
-    if (head_dim == 128)
-      hipLaunchKernelGGL((paged_decode_kernel<128, 2, seq_split_waves<128>()>), grid, block, 0,
-                         s, a);
-    else
-      hipLaunchKernelGGL((paged_decode_kernel<64, 2, seq_split_waves<64>()>), grid, block, 0, s,
-                         a);
+    const void* fn = head_dim == 128
+                         ? (app ? seq_split_kernel_fn<128, true>() : seq_split_kernel_fn<128>())
+                         : (app ? seq_split_kernel_fn<64, true>() : seq_split_kernel_fn<64>());
+    if (hipLaunchKernel(fn, grid, dim3(64 * lay.seq_split), args, 0, s) != hipSuccess) {
+      (void)hipGetLastError();
+      return NDL_ERR_LAUNCH;
+    }
     return check_launch();
   }
   const int depth = decode_pipeline_depth();
-  if (head_dim == 128) {
-    if (depth == 2)
-      hipLaunchKernelGGL((paged_decode_kernel<128, 2, 1>), grid, dim3(64), 0, s, a);
-    else if (depth == 4)
-      hipLaunchKernelGGL((paged_decode_kernel<128, 4, 1>), grid, dim3(64), 0, s, a);
-    else
-      hipLaunchKernelGGL((paged_decode_kernel<128, 3, 1>), grid, dim3(64), 0, s, a);
-  } else {
-    if (depth == 2)
-      hipLaunchKernelGGL((paged_decode_kernel<64, 2, 1>), grid, dim3(64), 0, s, a);
-    else if (depth == 4)
-      hipLaunchKernelGGL((paged_decode_kernel<64, 4, 1>), grid, dim3(64), 0, s, a);
-    else
-      hipLaunchKernelGGL((paged_decode_kernel<64, 3, 1>), grid, dim3(64), 0, s, a);
+  const void* fn = head_dim == 128
+                       ? (app ? decode_kernel_fn<128, true>(depth) : decode_kernel_fn<128>(depth))
+                       : (app ? decode_kernel_fn<64, true>(depth) : decode_kernel_fn<64>(depth));
+  if (hipLaunchKernel(fn, grid, dim3(64), args, 0, s) != hipSuccess) {
+    (void)hipGetLastError();
+    return NDL_ERR_LAUNCH;
   }
   int rc = check_launch();
   if (rc != NDL_OK) return rc;
@@ -756,4 +797,42 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
   else
     hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, s, a);
   return check_launch();
+}
+
+}  // namespace ndl
+
+extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
+                                const void* kv_cache, int64_t num_blocks,
+                                const int32_t* block_table, int64_t bt_row_stride,
+                                int max_blocks_per_seq, const int32_t* context_lens, int num_seqs,
+                                int num_heads, int num_kv_heads, int head_dim, int block_size,
+                                int dtype, float scale, int partition_tokens, void* workspace,
+                                size_t workspace_bytes, ndl_stream_t stream) {
+  return ndl::launch_decode(out, q, q_tok_stride, kv_cache, num_blocks, block_table,
+                            bt_row_stride, max_blocks_per_seq, context_lens, num_seqs, num_heads,
+                            num_kv_heads, head_dim, block_size, dtype, scale, partition_tokens,
+                            workspace, workspace_bytes, nullptr, 0, nullptr, 0, stream);
+}
+
+extern "C" int ndl_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
+                                       const void* k, int64_t k_tok_stride, const void* v,
+                                       int64_t v_tok_stride, void* kv_cache, int64_t num_blocks,
+                                       const int32_t* block_table, int64_t bt_row_stride,
+                                       int max_blocks_per_seq, const int32_t* context_lens,
+                                       int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                                       int block_size, int dtype, float scale,
+                                       int partition_tokens, void* workspace,
+                                       size_t workspace_bytes, ndl_stream_t stream) {
+  using namespace ndl;
+  if (num_seqs > 0) {
+    if (!k || !v) return NDL_ERR_INVALID_ARG;
+    if (((uintptr_t)k | (uintptr_t)v) & 15u) return NDL_ERR_INVALID_ARG;
+    if (k_tok_stride < (int64_t)num_kv_heads * head_dim ||
+        v_tok_stride < (int64_t)num_kv_heads * head_dim || ((k_tok_stride | v_tok_stride) & 7))
+      return NDL_ERR_INVALID_ARG;
+  }
+  return launch_decode(out, q, q_tok_stride, kv_cache, num_blocks, block_table, bt_row_stride,
+                       max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads,
+                       head_dim, block_size, dtype, scale, partition_tokens, workspace,
+                       workspace_bytes, k, k_tok_stride, v, v_tok_stride, stream);
 }

@@ -15,8 +15,8 @@ q and k already rotated, for callers that apply RoPE themselves
 (fuse_rope = False selects them inside forward):
 
   _prefill  (attention.py:102-107): ndl_kv_append (varlen) + ndl_varlen_prefill
-  _decode   (attention.py:140-159): ndl_kv_append (one token per sequence)
-                                    + ndl_paged_decode
+  _decode   (attention.py:140-159): ndl_paged_decode_append (the one-token-per-sequence
+                                    append and the attention in one launch)
 
 No host synchronisation happens on either path: the decode split-K grid is
 sized from block_table's width, prefill from max_seqlen (both host-known).
@@ -107,10 +107,9 @@ class Attention(nn.Module):
                                   self.num_kv_heads, self.head_dim)
 
     def _decode(self, q, k, v, kv_cache, block_table, context_lens):
-        ops.kv_append(k, v, kv_cache, block_table, context_lens)
-        return self._decode_attend(q, kv_cache, block_table, context_lens)
+        return self._decode_attend(q, kv_cache, block_table, context_lens, new_k=k, new_v=v)
 
-    def _decode_attend(self, q, kv_cache, block_table, context_lens):
+    def _decode_attend(self, q, kv_cache, block_table, context_lens, new_k=None, new_v=None):
         need = ops.decode_workspace_bytes(q.shape[0], self.num_heads, self.num_kv_heads,
                                           self.head_dim, block_table.shape[1], kv_cache.shape[3])
         ws = self._workspace
@@ -118,4 +117,4 @@ class Attention(nn.Module):
             ws = self._workspace = ops.decode_workspace(need, q.device)
         return ops.paged_decode(q, kv_cache, block_table, context_lens, self.scale,
                                 self.num_heads, self.num_kv_heads, self.head_dim,
-                                workspace=ws)
+                                workspace=ws, new_k=new_k, new_v=new_v)

@@ -194,13 +194,20 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
                  context_lens: torch.Tensor, scale: float, num_heads: int, num_kv_heads: int,
                  head_dim: int, *, partition_tokens: int = 0,
                  out: Optional[torch.Tensor] = None,
-                 workspace: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 workspace: Optional[torch.Tensor] = None,
+                 new_k: Optional[torch.Tensor] = None,
+                 new_v: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Paged decode attention; same signature as _decode_pytorch (attention.py:291).
 
     Sequence i attends min(context_lens[i] + 1, W * block_size) cached tokens.
     Returns [num_seqs, num_heads, head_dim] in q's dtype.  partition_tokens: 0 lets the
     library choose the split; -1 asks for one 8-wave workgroup per (kv head, sequence);
     a positive multiple of 16 asks for the stream split with that many tokens per wave.
+
+    new_k / new_v ([num_seqs, num_kv_heads, head_dim]): the decode append of this step
+    (attention.py:141-154) done in the same launch, with the same cache bytes and output as
+    kv_append followed by paged_decode.  Requires that no two sequences attend the same
+    block (as BlockAllocator's tables guarantee).
     """
     _check_cache(kv_cache)
     dev = kv_cache.device
@@ -230,13 +237,28 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
     _require(need > 0, "unsupported decode shape")
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = decode_workspace(need, dev)
-    rc = lib.ndl_paged_decode(
-        out.data_ptr(), q.data_ptr(), qs, kv_cache.data_ptr(), num_blocks,
-        block_table.data_ptr(), block_table.stride(0), w,
+    if new_k is None and new_v is None:
+        rc = lib.ndl_paged_decode(
+            out.data_ptr(), q.data_ptr(), qs, kv_cache.data_ptr(), num_blocks,
+            block_table.data_ptr(), block_table.stride(0), w,
+            context_lens.data_ptr(), n_seqs, num_heads, num_kv_heads, head_dim, bs,
+            _DTYPES[q.dtype], float(scale), partition_tokens, workspace.data_ptr(), need,
+            _stream(dev))
+        _lib.check(rc, "ndl_paged_decode")
+        return out
+    _require(new_k is not None and new_v is not None, "new_k and new_v go together")
+    for name, x in (("new_k", new_k), ("new_v", new_v)):
+        _require(x.dtype == kv_cache.dtype, f"{name} dtype must match kv_cache", TypeError)
+        _require(x.shape[0] == n_seqs, f"{name} must have one row per sequence")
+    ks = _rows("new_k", new_k, num_kv_heads, head_dim, dev)
+    vs = _rows("new_v", new_v, num_kv_heads, head_dim, dev)
+    rc = lib.ndl_paged_decode_append(
+        out.data_ptr(), q.data_ptr(), qs, new_k.data_ptr(), ks, new_v.data_ptr(), vs,
+        kv_cache.data_ptr(), num_blocks, block_table.data_ptr(), block_table.stride(0), w,
         context_lens.data_ptr(), n_seqs, num_heads, num_kv_heads, head_dim, bs,
         _DTYPES[q.dtype], float(scale), partition_tokens, workspace.data_ptr(), need,
         _stream(dev))
-    _lib.check(rc, "ndl_paged_decode")
+    _lib.check(rc, "ndl_paged_decode_append")
     return out
 
 
