@@ -157,8 +157,11 @@ __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
 // NW == 1: one wave per workgroup, wave s of a kv head takes stream tiles s*C .. s*C + C.
 // NW > 1: one workgroup per (kv head, sequence); wave w takes tiles w*C .. w*C + C of
 // the sequence (C = ceil(n / NW)) and the waves combine through LDS.
+// Two waves per SIMD for the default two-deep stream kernel (its 256-register budget), so
+// that the fused append's few extra registers do not halve its occupancy.
 template <int D, int NBUF, int NW, bool APP>
-__global__ __launch_bounds__(64 * NW) void paged_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
+    NW == 1 && NBUF == 2 ? 2 : 1))) void paged_decode_kernel(DecodeArgs a) {
   constexpr int KS = D / 32;   // k-steps of the QK^T MFMA
   constexpr int DPL = D / 16;  // head_dim elements per lane per V row
   constexpr int E = 4 * DPL;   // accumulator elements per lane (head_dim E*j .. + E of head c)
@@ -250,14 +253,19 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_kernel(DecodeArgs a) {
     // table row clamps).  The wave that owns that tile writes the row into the cache and
     // uses it in place of the row it loaded; no other wave reads the tile.  Each lane loads
     // the pieces of the new rows it holds in the tile layouts: chunk k_chunk of K, head_dim
-    // DPL*c .. of V.
+    // DPL*c .. of V.  The row is stored while the segment's first tile computes: stores
+    // count in the in-order memory counter, and stored there, only loads issued after it
+    // (a tile later) wait for it.
     const bool app = APP && lt1 == n_tiles;   // wave-uniform
     const int r_new = app ? a.context_lens[seq] & 15 : 0;
     u32x4 k_app = {0u, 0u, 0u, 0u};
     VT v_app = {};
+    int64_t app_blk = -1;   // the last tile's block (its table column), if valid
     if (app) {
       k_app = ld16(a.k_new + (int64_t)seq * a.k_new_stride + (int64_t)kvh * D + 8 * k_chunk);
       v_app = load_vrow<D>(a.v_new + (int64_t)seq * a.v_new_stride + (int64_t)kvh * D + DPL * c);
+      const int64_t b = a.block_table[(int64_t)seq * a.bt_row_stride + n_tiles - 1];
+      app_blk = b >= 0 && b < a.num_blocks ? b : -1;
     }
 
     f32x4 acc[DPL];
@@ -283,16 +291,9 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_kernel(DecodeArgs a) {
       };
 
       auto compute_tile = [&](int it, Tile& t) {
-        if (app && w0 + it == n_tiles - 1 && !t.bad) {   // the appended token's tile
-          const int64_t blk = __builtin_amdgcn_readlane(bt_lane, it);
-          u16* const kb = const_cast<u16*>(a.kplane) + blk * blk_stride + head_off + r_new * D;
-          u16* const vb = const_cast<u16*>(a.vplane) + blk * blk_stride + head_off + r_new * D;
-#pragma unroll
-          for (int s = 0; s < KS; ++s)
-            if (RPI * s + k_row == r_new) t.k[s] = k_app;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (4 * j + i == r_new) t.v[i] = v_app;
+        if (app && w0 + it == lt0 && app_blk >= 0) {   // the segment's first tile: the store
+          u16* const kb = const_cast<u16*>(a.kplane) + app_blk * blk_stride + head_off + r_new * D;
+          u16* const vb = const_cast<u16*>(a.vplane) + app_blk * blk_stride + head_off + r_new * D;
           if (k_row == r_new % RPI) st16(kb + 8 * k_chunk, k_app);
           if (j == (r_new >> 2)) {
             if constexpr (D == 128)
@@ -300,6 +301,14 @@ __global__ __launch_bounds__(64 * NW) void paged_decode_kernel(DecodeArgs a) {
             else
               *reinterpret_cast<VT*>(vb + DPL * c) = v_app;
           }
+        }
+        if (app && w0 + it == n_tiles - 1 && !t.bad) {   // the appended token's tile
+#pragma unroll
+          for (int s = 0; s < KS; ++s)
+            if (RPI * s + k_row == r_new) t.k[s] = k_app;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (4 * j + i == r_new) t.v[i] = v_app;
         }
         __builtin_amdgcn_wave_barrier();  // previous block's LDS reads are issued first
 #pragma unroll
