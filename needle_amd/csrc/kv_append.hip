@@ -135,16 +135,8 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
   // As few tokens per wave as keep every wave resident at once (a second, partial round
   // of waves costs more than longer waves: 17,705 tokens of 4 x 128 went 13.3 us at 1
   // or 2 tokens per wave, 12.9 us at 3, 14.1 us at 4 on MI355X).
-  static int64_t resident = [] {
-    int dev = 0, cus = 0, per_cu = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, (const void*)kv_append_kernel,
-                                                     256, 0) != hipSuccess ||
-        cus <= 0 || per_cu <= 0)
-      return (int64_t)8192;
-    return (int64_t)cus * per_cu * 4;
-  }();
+  int64_t resident = resident_workgroups((const void*)kv_append_kernel, 256) * 4;
+  if (resident <= 0) resident = 8192;
   int64_t tpw64 = (num_tokens + resident - 1) / resident;
   const int tpw = (int)(tpw64 < 1 ? 1 : tpw64 > kAppendMaxTokensPerWave ? kAppendMaxTokensPerWave
                                                                         : tpw64);

@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "../../include/needle_amd.h"
 
 namespace ndl {
@@ -62,6 +64,34 @@ __device__ __forceinline__ void st16(void* p, u32x4 v) { *reinterpret_cast<u32x4
 
 inline int check_launch() {
   return hipGetLastError() == hipSuccess ? NDL_OK : NDL_ERR_LAUNCH;
+}
+
+// Workgroups of `fn`, launched with `block` threads, that can be resident at once on the
+// current device (CUs times workgroups per CU); 0 when the device cannot be queried.  The
+// answer is cached per (kernel, block size, device) under a lock: the entry points may be
+// called from several host threads at once.
+inline int64_t resident_workgroups(const void* fn, int block) {
+  struct Entry { const void* fn; int block; int dev; int64_t wgs; };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  {
+    std::lock_guard<std::mutex> lock(mu);
+    for (int i = 0; i < used; ++i)
+      if (cache[i].fn == fn && cache[i].block == block && cache[i].dev == dev)
+        return cache[i].wgs;
+  }
+  int cus = 0, per_cu = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, 0) != hipSuccess ||
+      cus <= 0 || per_cu <= 0)
+    return 0;
+  const int64_t wgs = (int64_t)cus * per_cu;
+  std::lock_guard<std::mutex> lock(mu);
+  if (used < 64) cache[used++] = Entry{fn, block, dev, wgs};
+  return wgs;
 }
 
 }  // namespace ndl

@@ -602,24 +602,10 @@ inline int decode_pipeline_depth() {
 }
 
 // Resident waves of an attention kernel launched with `block` threads per workgroup on
-// the current device (CUs times workgroups per CU times waves per workgroup), cached per
-// device and kernel; 0 when the device cannot be queried.
+// the current device (CUs times workgroups per CU times waves per workgroup); 0 when the
+// device cannot be queried.
 inline int64_t decode_resident_waves(const void* fn, int block = 64) {
-  struct Entry { const void* fn; int dev; int64_t waves; };
-  static Entry cache[32];
-  static int used = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  for (int i = 0; i < used; ++i)
-    if (cache[i].fn == fn && cache[i].dev == dev) return cache[i].waves;
-  int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, 0) != hipSuccess ||
-      cus <= 0 || per_cu <= 0)
-    return 0;
-  const int64_t waves = (int64_t)cus * per_cu * (block / 64);
-  if (used < 32) cache[used++] = Entry{fn, dev, waves};
-  return waves;
+  return resident_workgroups(fn, block) * (block / 64);
 }
 
 // APP: with the fused append (a separate instantiation, so that the attention-only kernel

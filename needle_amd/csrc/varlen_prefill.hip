@@ -819,25 +819,6 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   }
 }
 
-// Workgroups of `fn` that can be resident at once on the current device (CUs times
-// workgroups per CU), cached per device and block size.
-inline int resident_slots(const void* fn, int block) {
-  struct Entry { const void* fn; int block; int dev; int slots; };
-  static Entry cache[32];
-  static int used = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return -1;
-  for (int i = 0; i < used; ++i)
-    if (cache[i].fn == fn && cache[i].block == block && cache[i].dev == dev) return cache[i].slots;
-  int cus = 0, per_cu = 0;
-  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-      hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, fn, block, 0) != hipSuccess)
-    return -1;
-  const int slots = cus * (per_cu > 0 ? per_cu : 1);
-  if (used < 32) cache[used++] = Entry{fn, block, dev, slots};
-  return slots;
-}
-
 }  // namespace ndl
 
 extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
@@ -910,7 +891,7 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
                                    : (const void*)varlen_prefill_kernel<64, 8>;
   dim3 grid((unsigned)gx, (unsigned)num_seqs, (unsigned)qtiles);
   if (a.persistent) {
-    const int slots = resident_slots(fn, 64 * waves);
+    const int64_t slots = resident_workgroups(fn, 64 * waves);
     if (slots <= 0) return NDL_ERR_LAUNCH;
     const int64_t items = gx * (int64_t)num_seqs * qtiles;   // upper bound of the list
     grid = dim3((unsigned)(items < slots ? items : slots), 1, 1);
