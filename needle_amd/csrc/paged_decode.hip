@@ -142,6 +142,12 @@ __device__ __forceinline__ void stream_locate(const DecodeArgs& a, int lane, int
 
 // Tiles per wave: the fixed chunk, or the stream length (tiles of all sequences of one
 // kv head) over the waves of a kv head, at least kDecodeMinChunk.
+// The chunk for a stream of `total` tiles.
+__device__ __forceinline__ int64_t stream_chunk_of(const DecodeArgs& a, int64_t total) {
+  if (a.chunk > 0) return a.chunk;
+  const int64_t c = (total + a.waves - 1) / a.waves;
+  return c < kDecodeMinChunk ? kDecodeMinChunk : c;
+}
 __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
   if (a.chunk > 0) return a.chunk;
   int64_t total = 0;
@@ -150,8 +156,7 @@ __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
     const int n = q < a.num_seqs ? seq_tiles(a, q) : 0;
     total += __builtin_amdgcn_readlane(wave_incl_scan(n, lane), 63);
   }
-  const int64_t c = (total + a.waves - 1) / a.waves;
-  return c < kDecodeMinChunk ? kDecodeMinChunk : c;
+  return stream_chunk_of(a, total);
 }
 
 // NW == 1: one wave per workgroup, wave s of a kv head takes stream tiles s*C .. s*C + C.
@@ -518,7 +523,21 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
   const int kvh = head / a.group, hc = head - kvh * a.group;
   u16* dst = a.out + ((int64_t)seq * a.num_heads + head) * D + lane * PER_LANE;
-  const int nt = seq_tiles(a, seq);
+  // One pass over context_lens (one load per 64 sequences, nothing else in flight before
+  // it): this sequence's tiles, its first stream tile and the stream's total, i.e. what
+  // seq_tiles, stream_locate and stream_chunk give.
+  int nt = 0;
+  int64_t first = 0, total = 0;
+  for (int base = 0; base < a.num_seqs; base += 64) {
+    const int q = base + lane;
+    const int n = q < a.num_seqs ? seq_tiles(a, q) : 0;
+    const int incl = wave_incl_scan(n, lane);
+    if (seq >= base && seq < base + 64) {
+      nt = __builtin_amdgcn_readlane(n, seq - base);
+      first = total + __builtin_amdgcn_readlane(incl - n, seq - base);
+    }
+    total += __builtin_amdgcn_readlane(incl, 63);
+  }
   if (nt == 0) {
     if constexpr (PER_LANE == 2)
       *reinterpret_cast<uint32_t*>(dst) = 0u;
@@ -526,10 +545,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
       dst[0] = 0;
     return;
   }
-  int found;
-  int64_t first;
-  stream_locate(a, lane, seq, 0, &found, &first);
-  const int64_t chunk = stream_chunk(a, lane);
+  const int64_t chunk = stream_chunk_of(a, total);
   const int64_t s0 = first / chunk, s1 = (first + nt - 1) / chunk;
   if (s0 == s1) return;
   const int nparts = (int)(s1 - s0 + 1);
