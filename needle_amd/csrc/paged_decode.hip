@@ -430,14 +430,30 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
   };
 
   if constexpr (NW == 1) {
-    // Walk the sequences that own tiles start .. end of this kv head's stream.
-    const int64_t chunk = stream_chunk(a, lane);
-    const int64_t start = (int64_t)sw * chunk, end = start + chunk;
+    // Walk the sequences that own tiles start .. end of this kv head's stream.  Up to 64
+    // sequences, one load gives every sequence's tiles (lane i: sequence i): the chunk,
+    // the first sequence and each sequence's tiles then come from registers.
+    const bool one_load = a.num_seqs <= 64;
+    int n_lane = 0;
+    int64_t chunk, first;
     int seq;
-    int64_t first;
-    stream_locate(a, lane, -1, start, &seq, &first);
+    if (one_load) {
+      n_lane = lane < a.num_seqs ? seq_tiles(a, lane) : 0;
+      const int incl = wave_incl_scan(n_lane, lane);
+      const int total = __builtin_amdgcn_readlane(incl, 63);
+      chunk = stream_chunk_of(a, total);
+      const int64_t tile = (int64_t)sw * chunk;
+      const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < a.num_seqs && n_lane > 0 &&
+                                                       (int64_t)incl > tile);
+      seq = hit ? __builtin_ctzll(hit) : a.num_seqs;
+      first = hit ? __builtin_amdgcn_readlane(incl - n_lane, seq) : total;
+    } else {
+      chunk = stream_chunk(a, lane);
+      stream_locate(a, lane, -1, (int64_t)sw * chunk, &seq, &first);
+    }
+    const int64_t start = (int64_t)sw * chunk, end = start + chunk;
     while (seq < a.num_seqs && first < end) {
-      const int nt = seq_tiles(a, seq);
+      const int nt = one_load ? __builtin_amdgcn_readlane(n_lane, seq) : seq_tiles(a, seq);
       if (nt > 0) {
         const int64_t s0 = start > first ? start : first;
         const int64_t s1 = end < first + nt ? end : first + nt;

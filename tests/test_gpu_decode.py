@@ -251,3 +251,34 @@ def test_graph_replays_of_two_batch_sizes_share_a_workspace():
         assert torch.equal(out.float().cpu(), refs[id(c)])
         other = order[(n + 1) % len(order)]
         assert torch.equal(call(other, ws).float().cpu(), refs[id(other)])
+
+
+@pytest.mark.parametrize("part", [0, 64])
+@pytest.mark.parametrize("nseq", [63, 64, 65, 130])
+def test_batch_sizes_around_one_wave_of_sequences(nseq, part):
+    """The stream split reads the context lengths with one load up to 64 sequences and
+    scans them 64 at a time beyond; both sides of that boundary, with empty sequences at
+    the edges of the 64-sequence chunks, against the oracle (the merge walks the same
+    lengths)."""
+    rng = np.random.default_rng(300 + nseq)
+    ctx = rng.integers(0, 600, size=nseq).tolist()
+    case = wl.decode_case(wl.LLAMA3_8B, ctx, seed=310 + nseq, garbage=False)
+    for i in (0, 63, 64, nseq - 1):
+        if i < nseq:
+            ctx[i] = -1
+    case.context_lens = torch.tensor(ctx, dtype=torch.int32)
+    case.ctx = list(ctx)
+    s = case.shape
+    g = case.to(DEV)
+    out = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
+                           s.num_heads, s.num_kv_heads, s.head_dim, partition_tokens=part)
+    torch.cuda.synchronize()
+    got = out.float().cpu()
+    empty = [i for i in range(nseq) if ctx[i] < 0]
+    live = [i for i in range(nseq) if ctx[i] >= 0]
+    for i in empty:
+        assert torch.equal(got[i], torch.zeros_like(got[i]))
+    want = paged_ref.decode_pytorch(case.q[live], case.kv_cache, case.block_table[live],
+                                    case.context_lens[live], s.scale, s.num_heads,
+                                    s.num_kv_heads, s.head_dim)
+    assert_close(got[live], want.float())
