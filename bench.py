@@ -289,9 +289,47 @@ def ceilings(torch):
         warm(torch, fn, 1.0)
         ms = time_region(torch, fn, 10)
         res[name] = round(work / (ms / 1e3) / (1e9 if unit == "GB" else 1e12), 1)
+    del x, y, a, b
+    res["sdpa_flash_qwen2_7b_prefill_tflops"] = sdpa_ceiling(torch)
     res["hbm_peak_gbs"] = HBM_PEAK_GBS
     res["mfma_bf16_peak_tflops"] = MFMA_BF16_PEAK_TFLOPS
     return res
+
+
+def sdpa_ceiling(torch):
+    """torch's fused attention (the flash backend only) on the Qwen2-7B prefill prompts:
+    dense, contiguous per-prompt q / k / v with the kv heads expanded, causal, one call per
+    prompt; the same algorithmic flops as the paged prefill.  None when the flash backend
+    is unavailable (the math fallback is never run)."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    import torch.nn.functional as fnn
+    from needle_amd import workloads as wl
+    dev = torch.device("cuda:0")
+    shape = wl.QWEN2_7B
+    lens = wl.qwen7b_prefill_lens()
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED)
+    h, hkv, d = shape.num_heads, shape.num_kv_heads, shape.head_dim
+    qkv = []
+    for n in lens:
+        q = torch.randn(1, h, n, d, device=dev, dtype=torch.bfloat16, generator=gen)
+        k = torch.randn(1, hkv, n, d, device=dev, dtype=torch.bfloat16, generator=gen)
+        v = torch.randn(1, hkv, n, d, device=dev, dtype=torch.bfloat16, generator=gen)
+        qkv.append((q, k.repeat_interleave(h // hkv, dim=1).contiguous(),
+                    v.repeat_interleave(h // hkv, dim=1).contiguous()))
+
+    def run():
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+            for q, k, v in qkv:
+                fnn.scaled_dot_product_attention(q, k, v, is_causal=True)
+    try:
+        run()
+        torch.cuda.synchronize()
+    except RuntimeError:
+        return None
+    warm(torch, run, 1.0)
+    ms = time_region(torch, run, 10)
+    return round(wl.prefill_flops(shape, lens) / (ms / 1e3) / 1e12, 1)
 
 
 def cpu_baseline(torch, wl, shape, ctx, budget_s):
