@@ -166,10 +166,12 @@ int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
  *
  * Same cache bytes and the same out as ndl_kv_append (cu_seqlens NULL: k/v row i is
  * sequence i's token at position context_lens[i]) followed by ndl_paged_decode with
- * the same arguments: the wave that attends a sequence's last block writes the new row
- * there and attends it in place of the row it read.  k, v: [num_seqs][num_kv_heads]
- * [head_dim], token strides k_tok_stride / v_tok_stride (multiples of 8, 16-byte
- * aligned rows).  Requires that no block is attended by two sequences (BlockAllocator
+ * the same arguments: the wave that attends a sequence's last block attends the new row
+ * in place of the row it read, and the row is written to the cache within the same call
+ * (by the attending workgroup when each sequence has its own; otherwise by the kernel
+ * that merges the split sequences' partials, enqueued by the same call).  k, v:
+ * [num_seqs][num_kv_heads][head_dim], token strides k_tok_stride / v_tok_stride
+ * (multiples of 8, 16-byte aligned rows).  Requires that no block is attended by two sequences (BlockAllocator
  * hands every block to one sequence, block_allocator.py:37-56); the workspace is the
  * one ndl_paged_decode_workspace_bytes sizes.
  */

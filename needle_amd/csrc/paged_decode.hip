@@ -171,6 +171,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
   constexpr int DPL = D / 16;  // head_dim elements per lane per V row
   constexpr int E = 4 * DPL;   // accumulator elements per lane (head_dim E*j .. + E of head c)
   using VT = typename VRow<D>::T;
+  // With the fused append, the new row reaches the cache from this kernel when the
+  // workgroups are per sequence (NW > 1: no merge launch follows); in the stream split the
+  // merge kernel stores it, and this kernel only attends it from registers.
+  constexpr bool kStoreRow = APP && NW > 1;
 
   // kv head is the fastest grid index: the 8 head slices of one block (adjacent in
   // memory) are fetched by waves dispatched together.
@@ -269,8 +273,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     if (app) {
       k_app = ld16(a.k_new + (int64_t)seq * a.k_new_stride + (int64_t)kvh * D + 8 * k_chunk);
       v_app = load_vrow<D>(a.v_new + (int64_t)seq * a.v_new_stride + (int64_t)kvh * D + DPL * c);
-      const int64_t b = a.block_table[(int64_t)seq * a.bt_row_stride + n_tiles - 1];
-      app_blk = b >= 0 && b < a.num_blocks ? b : -1;
+      if constexpr (kStoreRow) {
+        const int64_t b = a.block_table[(int64_t)seq * a.bt_row_stride + n_tiles - 1];
+        app_blk = b >= 0 && b < a.num_blocks ? b : -1;
+      }
     }
 
     f32x4 acc[DPL];
@@ -296,7 +302,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       };
 
       auto compute_tile = [&](int it, Tile& t) {
-        if (app && w0 + it == lt0 && app_blk >= 0) {   // the segment's first tile: the store
+        if (kStoreRow && app && w0 + it == lt0 && app_blk >= 0) {   // the segment's first tile
           u16* const kb = const_cast<u16*>(a.kplane) + app_blk * blk_stride + head_off + r_new * D;
           u16* const vb = const_cast<u16*>(a.vplane) + app_blk * blk_stride + head_off + r_new * D;
           if (k_row == r_new % RPI) st16(kb + 8 * k_chunk, k_app);
@@ -538,6 +544,27 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   __shared__ float wsh[kMergeMaxParts];
   const int head = blockIdx.x, seq = blockIdx.y, lane = threadIdx.x;
   const int kvh = head / a.group, hc = head - kvh * a.group;
+  // The decode step's new K/V row (ndl_paged_decode_append): the attention kernel attended
+  // it from registers; the first query head's wave of each (kv head, sequence) stores it,
+  // with the separate append's rule (attention.py:141-154): column min(ctx / 16, W - 1),
+  // row ctx % 16, nothing for a negative context or an invalid block id.
+  if (a.k_new != nullptr && hc == 0) {
+    constexpr int CH = D / 8;   // 16-byte chunks per row; lanes < CH: K, < 2 CH: V
+    const int ctx = a.context_lens[seq];
+    if (ctx >= 0 && lane < 2 * CH) {
+      const int col = ctx / 16 < a.max_blocks - 1 ? ctx / 16 : a.max_blocks - 1;
+      const int64_t b = a.block_table[(int64_t)seq * a.bt_row_stride + col];
+      if (b >= 0 && b < a.num_blocks) {
+        const bool is_v = lane >= CH;
+        const int ch = is_v ? lane - CH : lane;
+        const u16* src = (is_v ? a.v_new + (int64_t)seq * a.v_new_stride
+                               : a.k_new + (int64_t)seq * a.k_new_stride) + (int64_t)kvh * D + 8 * ch;
+        u16* row = const_cast<u16*>(is_v ? a.vplane : a.kplane) +
+                   (b * a.num_kv_heads + kvh) * (int64_t)(16 * D) + (ctx & 15) * D + 8 * ch;
+        st16(row, ld16(src));
+      }
+    }
+  }
   u16* dst = a.out + ((int64_t)seq * a.num_heads + head) * D + lane * PER_LANE;
   // One pass over context_lens (one load per 64 sequences, nothing else in flight before
   // it): this sequence's tiles, its first stream tile and the stream's total, i.e. what
