@@ -46,15 +46,19 @@ extern "C" {
 /* Same object as hipStream_t; declared here so callers need no HIP headers. */
 typedef struct ihipStream_t* ndl_stream_t;
 
-#define NDL_ABI_VERSION 2
+#define NDL_ABI_VERSION 3
 
 enum ndl_status {
   NDL_OK = 0,
   NDL_ERR_INVALID_ARG = -1,   /* null pointer, negative size, inconsistent shape */
   NDL_ERR_UNSUPPORTED = -2,   /* dtype / head_dim / block_size / group size not built */
   NDL_ERR_WORKSPACE = -3,     /* workspace smaller than the *_workspace_bytes query */
-  NDL_ERR_LAUNCH = -4         /* the HIP runtime rejected a kernel launch */
+  NDL_ERR_LAUNCH = -4,        /* the HIP runtime rejected a kernel launch */
+  NDL_ERR_SCRATCH_LIMIT = -5  /* the shape needs more than NDL_DECODE_STATIC_SCRATCH_BYTES */
 };
+
+/* Size of the per-device static scratch array of ndl_paged_decode_append_noalloc. */
+#define NDL_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
 
 enum ndl_dtype {
   NDL_DTYPE_BF16 = 0,
@@ -184,6 +188,32 @@ int ndl_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
                             int num_heads, int num_kv_heads, int head_dim, int block_size,
                             int dtype, float scale, int partition_tokens,
                             void* workspace, size_t workspace_bytes, ndl_stream_t stream);
+
+/*
+ * ndl_paged_decode_append without a workspace argument and without any allocation.
+ *
+ * No counterpart in the reference: this entry point is for callers that cannot allocate
+ * device memory at the call (code under HIP graph capture, serving loops that forbid
+ * allocation).  It calls no hipMalloc/hipFree and no allocating library routine.  The
+ * split-K partials live in a static device array of NDL_DECODE_STATIC_SCRATCH_BYTES
+ * (16 MiB) per GPU, held until the process ends; a shape whose
+ * ndl_paged_decode_workspace_bytes exceeds that returns NDL_ERR_SCRATCH_LIMIT (the
+ * Llama-3-8B decode shapes need 5-9 MB).  Same arguments, kernels, cache bytes and out as
+ * ndl_paged_decode_append.  All calls on one GPU share that GPU's array: calls that
+ * overlap on one GPU (different streams, or different host threads without stream order
+ * between them) race and may return wrong results; calls in stream order are safe.  The
+ * first call on a device looks the array's address up (hipGetSymbolAddress) with that
+ * device current.
+ */
+int ndl_paged_decode_append_noalloc(void* out, const void* q, int64_t q_tok_stride,
+                                    const void* k, int64_t k_tok_stride,
+                                    const void* v, int64_t v_tok_stride,
+                                    void* kv_cache, int64_t num_blocks,
+                                    const int32_t* block_table, int64_t bt_row_stride,
+                                    int max_blocks_per_seq, const int32_t* context_lens,
+                                    int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                                    int block_size, int dtype, float scale,
+                                    int partition_tokens, ndl_stream_t stream);
 
 /*
  * Varlen causal prefill attention over the paged cache.

@@ -15,7 +15,8 @@ import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 _PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = _PKG_DIR / "libneedle_amd.so"
 
-NDL_ABI_VERSION = 2
+NDL_ABI_VERSION = 3
+NDL_DECODE_STATIC_SCRATCH_BYTES = 16 << 20
 NDL_DTYPE_BF16 = 0
 NDL_DTYPE_F16 = 1
 
@@ -28,6 +29,7 @@ EXPORTED_SYMBOLS = (
     "ndl_paged_decode_workspace_bytes",
     "ndl_paged_decode",
     "ndl_paged_decode_append",
+    "ndl_paged_decode_append_noalloc",
     "ndl_varlen_prefill",
 )
 
@@ -73,6 +75,15 @@ _SIGNATURES = {
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # H, Hkv, D, bs, dtype
         _c_f32, _c_i32,                                 # scale, partition
         _c_p, _c_sz, _c_p,                              # workspace, bytes, stream
+    ]),
+    "ndl_paged_decode_append_noalloc": (_c_i32, [
+        _c_p, _c_p, _c_i64,                             # out, q, q stride
+        _c_p, _c_i64, _c_p, _c_i64,                     # k, k stride, v, v stride
+        _c_p, _c_i64,                                   # cache, NB
+        _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
+        _c_p, _c_i32,                                   # ctx, B
+        _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # H, Hkv, D, bs, dtype
+        _c_f32, _c_i32, _c_p,                           # scale, partition, stream
     ]),
     "ndl_varlen_prefill": (_c_i32, [
         _c_p, _c_p, _c_i64,                             # out, q, q stride

@@ -10,6 +10,7 @@ extern "C" const char* ndl_strerror(int status) {
     case NDL_ERR_UNSUPPORTED: return "unsupported dtype, head_dim, block_size or group size";
     case NDL_ERR_WORKSPACE: return "workspace missing or too small";
     case NDL_ERR_LAUNCH: return "kernel launch failed";
+    case NDL_ERR_SCRATCH_LIMIT: return "shape needs more than the static decode scratch";
     default: return "unknown status";
   }
 }

@@ -759,13 +759,53 @@ extern "C" size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, 
 
 namespace ndl {
 
+// Allocation-free decode (ndl_paged_decode_append_noalloc): the split-K partials go to a
+// file-scope device array instead of a caller workspace.  Every GPU the library runs on
+// holds its own copy of the array (at its own address) until the process ends.  The host
+// name `scratch` is only a stand-in for the device symbol: kernels get the address that
+// hipGetSymbolAddress returns for the current device, looked up once per device and kept.
+// Nothing in the array needs to start at zero (the kernels write every partial they later
+// read), so no call clears it.
+constexpr size_t kStaticScratchBytes = NDL_DECODE_STATIC_SCRATCH_BYTES;
+constexpr int kStaticScratchDevices = 64;
+
+static __device__ __align__(256) unsigned char scratch[kStaticScratchBytes];
+
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kStaticScratchDevices] = {};
+
+// The device address of `scratch` on the current device (looked up on the first call per
+// device, with that device current).
+static int static_scratch_ptr(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    (void)hipGetLastError();
+    return NDL_ERR_LAUNCH;
+  }
+  if (dev < 0 || dev >= kStaticScratchDevices) return NDL_ERR_UNSUPPORTED;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
+      (void)hipGetLastError();
+      return NDL_ERR_LAUNCH;
+    }
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return NDL_OK;
+}
+
+// static_scratch: ignore workspace/workspace_bytes and use the static array (after every
+// argument check, so that a rejected call never touches the device).
 static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const void* kv_cache,
                          int64_t num_blocks, const int32_t* block_table, int64_t bt_row_stride,
                          int max_blocks_per_seq, const int32_t* context_lens, int num_seqs,
                          int num_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
                          float scale, int partition_tokens, void* workspace,
                          size_t workspace_bytes, const void* k_new, int64_t k_new_stride,
-                         const void* v_new, int64_t v_new_stride, ndl_stream_t stream) {
+                         const void* v_new, int64_t v_new_stride, ndl_stream_t stream,
+                         bool static_scratch = false) {
   if (dtype != NDL_DTYPE_BF16) return NDL_ERR_UNSUPPORTED;
   if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -792,6 +832,12 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   const int64_t grid_waves = lay.seq_split ? (int64_t)num_seqs * num_kv_heads
                                            : lay.waves * num_kv_heads;
   if (grid_waves > 0x7fffffff || lay.nseg > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
+  if (static_scratch) {
+    if (lay.bytes > kStaticScratchBytes) return NDL_ERR_SCRATCH_LIMIT;
+    const int rc = static_scratch_ptr(&workspace);
+    if (rc != NDL_OK) return rc;
+    workspace_bytes = kStaticScratchBytes;
+  }
   if (workspace == nullptr || workspace_bytes < lay.bytes || ((uintptr_t)workspace & 15u))
     return NDL_ERR_WORKSPACE;
 
@@ -868,16 +914,18 @@ extern "C" int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
                             workspace, workspace_bytes, nullptr, 0, nullptr, 0, stream);
 }
 
-extern "C" int ndl_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
-                                       const void* k, int64_t k_tok_stride, const void* v,
-                                       int64_t v_tok_stride, void* kv_cache, int64_t num_blocks,
-                                       const int32_t* block_table, int64_t bt_row_stride,
-                                       int max_blocks_per_seq, const int32_t* context_lens,
-                                       int num_seqs, int num_heads, int num_kv_heads, int head_dim,
-                                       int block_size, int dtype, float scale,
-                                       int partition_tokens, void* workspace,
-                                       size_t workspace_bytes, ndl_stream_t stream) {
-  using namespace ndl;
+namespace ndl {
+
+// The fused append's own argument checks, then the launch.
+static int launch_decode_append(void* out, const void* q, int64_t q_tok_stride, const void* k,
+                                int64_t k_tok_stride, const void* v, int64_t v_tok_stride,
+                                void* kv_cache, int64_t num_blocks, const int32_t* block_table,
+                                int64_t bt_row_stride, int max_blocks_per_seq,
+                                const int32_t* context_lens, int num_seqs, int num_heads,
+                                int num_kv_heads, int head_dim, int block_size, int dtype,
+                                float scale, int partition_tokens, void* workspace,
+                                size_t workspace_bytes, ndl_stream_t stream,
+                                bool static_scratch) {
   if (num_seqs > 0) {
     if (!k || !v) return NDL_ERR_INVALID_ARG;
     if (((uintptr_t)k | (uintptr_t)v) & 15u) return NDL_ERR_INVALID_ARG;
@@ -888,5 +936,38 @@ extern "C" int ndl_paged_decode_append(void* out, const void* q, int64_t q_tok_s
   return launch_decode(out, q, q_tok_stride, kv_cache, num_blocks, block_table, bt_row_stride,
                        max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads,
                        head_dim, block_size, dtype, scale, partition_tokens, workspace,
-                       workspace_bytes, k, k_tok_stride, v, v_tok_stride, stream);
+                       workspace_bytes, k, k_tok_stride, v, v_tok_stride, stream,
+                       static_scratch);
+}
+
+}  // namespace ndl
+
+extern "C" int ndl_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
+                                       const void* k, int64_t k_tok_stride, const void* v,
+                                       int64_t v_tok_stride, void* kv_cache, int64_t num_blocks,
+                                       const int32_t* block_table, int64_t bt_row_stride,
+                                       int max_blocks_per_seq, const int32_t* context_lens,
+                                       int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                                       int block_size, int dtype, float scale,
+                                       int partition_tokens, void* workspace,
+                                       size_t workspace_bytes, ndl_stream_t stream) {
+  return ndl::launch_decode_append(out, q, q_tok_stride, k, k_tok_stride, v, v_tok_stride,
+                                   kv_cache, num_blocks, block_table, bt_row_stride,
+                                   max_blocks_per_seq, context_lens, num_seqs, num_heads,
+                                   num_kv_heads, head_dim, block_size, dtype, scale,
+                                   partition_tokens, workspace, workspace_bytes, stream, false);
+}
+
+// Allocation-free form: the partials live in the static array `scratch` (see above).
+extern "C" int ndl_paged_decode_append_noalloc(
+    void* out, const void* q, int64_t q_tok_stride, const void* k, int64_t k_tok_stride,
+    const void* v, int64_t v_tok_stride, void* kv_cache, int64_t num_blocks,
+    const int32_t* block_table, int64_t bt_row_stride, int max_blocks_per_seq,
+    const int32_t* context_lens, int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+    int block_size, int dtype, float scale, int partition_tokens, ndl_stream_t stream) {
+  return ndl::launch_decode_append(out, q, q_tok_stride, k, k_tok_stride, v, v_tok_stride,
+                                   kv_cache, num_blocks, block_table, bt_row_stride,
+                                   max_blocks_per_seq, context_lens, num_seqs, num_heads,
+                                   num_kv_heads, head_dim, block_size, dtype, scale,
+                                   partition_tokens, nullptr, 0, stream, true);
 }

@@ -39,7 +39,7 @@ def test_every_declared_symbol_is_exported(lib):
 def test_version_and_status_text(lib):
     assert lib.ndl_abi_version() == _lib.NDL_ABI_VERSION
     assert lib.ndl_strerror(0) == b"ok"
-    for code in (-1, -2, -3, -4):
+    for code in (-1, -2, -3, -4, -5):
         assert lib.ndl_strerror(code) and lib.ndl_strerror(code) != b"unknown status"
     assert lib.ndl_strerror(-99) == b"unknown status"
 
@@ -97,6 +97,20 @@ def test_rejections_before_any_launch(lib):
     assert rope(d=72) == -2
     assert rope(t=0) == 0
     assert rope() == -1
+    # the allocation-free decode: a shape whose partials exceed the static array is refused
+    # after the argument checks and before any device call (1000 sequences x 1000 blocks at
+    # 16 tokens per wave); the aligned stand-in addresses are never dereferenced
+    assert lib.ndl_paged_decode_workspace_bytes(1000, 32, 8, 128, 1000, 16, 16) > \
+        _lib.NDL_DECODE_STATIC_SCRATCH_BYTES
+    fake = 1 << 20
+    rc = lib.ndl_paged_decode_append_noalloc(fake, fake, 4096, fake, 1024, fake, 1024, fake,
+                                             16000, fake, 1000, 1000, fake, 1000, 32, 8, 128, 16,
+                                             0, 1.0, 16, None)
+    assert rc == -5 and lib.ndl_strerror(rc) != b"unknown status"
+    # ... and an unsupported shape gets the workspace entry point's own status
+    rc = lib.ndl_paged_decode_append_noalloc(None, None, 4096, None, 1024, None, 1024, None, 1,
+                                             None, 1, 1, None, 1, 32, 8, 96, 16, 0, 1.0, 0, None)
+    assert rc == -1 or rc == -2
     # nothing to do: zero tokens / sequences
     assert lib.ndl_kv_append(None, 1, 1, 16, 128, 0, None, 128, None, 128, None, 1, 1, None,
                              None, 1, 0, None) == 0
