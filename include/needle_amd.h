@@ -13,9 +13,13 @@
  *                        also covers the FlashInfer wrapper :161-197)
  *   ndl_paged_decode_append  the decode append and that attention in one launch
  *                       (_decode :141-159)
+ *   ndl_rope_paged_decode_append  the same with the rotary embedding of q and of the
+ *                       new key row folded in (:88 then _decode :141-159)
  *   ndl_varlen_prefill  causal attention of packed varlen prompts, reading K/V
  *                       back through block_table
  *                       (_prefill_pytorch :120-134; FlashInfer path :109-118)
+ *   ndl_kv_block_copy   whole-block copies between pools for the KV swap
+ *                       (needle/model/runner.py:175-192)
  *
  * Conventions (every entry point):
  *   - Plain pointers to device memory, element counts and strides in ELEMENTS.
@@ -46,7 +50,7 @@ extern "C" {
 /* Same object as hipStream_t; declared here so callers need no HIP headers. */
 typedef struct ihipStream_t* ndl_stream_t;
 
-#define NDL_ABI_VERSION 3
+#define NDL_ABI_VERSION 4
 
 enum ndl_status {
   NDL_OK = 0,
@@ -190,6 +194,31 @@ int ndl_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
                             void* workspace, size_t workspace_bytes, ndl_stream_t stream);
 
 /*
+ * The decode step of Attention.forward from RoPE on: the rotary embedding of q and of the
+ * step's new key row, the append of the new k/v rows and the paged attention, in one
+ * launch (plus the merge launch of the stream split).
+ *
+ * Replaces: needle/layers/attention.py:88 (_apply_rope :277-288 on the decode tokens)
+ *           followed by _decode :141-159 (append :141-154, _decode_pytorch :291-310).
+ *
+ * q, k: as produced by the projections, NOT rotated.  cos/sin: [num_seqs][head_dim] rows
+ * of the new tokens (the model's get_cos_sin(positions)), token stride cs_tok_stride.  The
+ * rotation is ndl_rope_kv_append's, bit for bit (the reference's bf16 rounding op for op),
+ * so the cache bytes and out equal those of ndl_rope_kv_append (decode form) followed by
+ * ndl_paged_decode with the rotated q.  Everything else as ndl_paged_decode_append.
+ */
+int ndl_rope_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
+                                 const void* k, int64_t k_tok_stride,
+                                 const void* v, int64_t v_tok_stride,
+                                 const void* cos, const void* sin, int64_t cs_tok_stride,
+                                 void* kv_cache, int64_t num_blocks,
+                                 const int32_t* block_table, int64_t bt_row_stride,
+                                 int max_blocks_per_seq, const int32_t* context_lens,
+                                 int num_seqs, int num_heads, int num_kv_heads, int head_dim,
+                                 int block_size, int dtype, float scale, int partition_tokens,
+                                 void* workspace, size_t workspace_bytes, ndl_stream_t stream);
+
+/*
  * ndl_paged_decode_append without a workspace argument and without any allocation.
  *
  * No counterpart in the reference: this entry point is for callers that cannot allocate
@@ -240,6 +269,29 @@ int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
                        int num_seqs, int64_t num_tokens, int max_seqlen, int max_context_len,
                        int num_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
                        float scale, ndl_stream_t stream);
+
+/*
+ * Copy whole KV blocks between two sets of per-layer pools: the swap-out (GPU pool ->
+ * pinned CPU pool) and swap-in (CPU pool -> GPU pool) copies of a preemption.
+ *
+ * Replaces: needle/model/runner.py:175-192 (_swap_kv_blocks: one copy per layer and block),
+ *           fed by BlockAllocator.swap_out / swap_in (block_allocator.py:88-106).
+ *
+ * For every layer l < num_layers, pair j < num_pairs and plane p (K, V):
+ *   dst_pools[l][p][dst_ids[j]][:][:][:] = src_pools[l][p][src_ids[j]][:][:][:]
+ * Pools are [2][num_blocks][num_kv_heads][block_size][head_dim] (16-byte aligned), in
+ * device memory or in pinned host memory (hipHostMalloc, torch pin_memory=True), which the
+ * kernel reads or writes through its device mapping; other host memory is rejected
+ * (NDL_ERR_INVALID_ARG) before any launch.  src_ids / dst_ids: int32 [num_pairs] in device
+ * memory or pinned host memory.  A pair with an id outside its pool is skipped.  Pairs
+ * must not write one destination block twice.  One launch for all layers;
+ * num_layers <= 128.  bf16 or fp16 (the copy is bit-exact either way).
+ */
+int ndl_kv_block_copy(void* const* dst_pools, int64_t dst_num_blocks,
+                      const void* const* src_pools, int64_t src_num_blocks,
+                      int num_layers, int num_kv_heads, int block_size, int head_dim, int dtype,
+                      const int32_t* src_ids, const int32_t* dst_ids, int num_pairs,
+                      ndl_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 _PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = _PKG_DIR / "libneedle_amd.so"
 
-NDL_ABI_VERSION = 3
+NDL_ABI_VERSION = 4
 NDL_DECODE_STATIC_SCRATCH_BYTES = 16 << 20
 NDL_DTYPE_BF16 = 0
 NDL_DTYPE_F16 = 1
@@ -30,7 +30,9 @@ EXPORTED_SYMBOLS = (
     "ndl_paged_decode",
     "ndl_paged_decode_append",
     "ndl_paged_decode_append_noalloc",
+    "ndl_rope_paged_decode_append",
     "ndl_varlen_prefill",
+    "ndl_kv_block_copy",
 )
 
 _c_i32 = ctypes.c_int
@@ -85,6 +87,17 @@ _SIGNATURES = {
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # H, Hkv, D, bs, dtype
         _c_f32, _c_i32, _c_p,                           # scale, partition, stream
     ]),
+    "ndl_rope_paged_decode_append": (_c_i32, [
+        _c_p, _c_p, _c_i64,                             # out, q, q stride
+        _c_p, _c_i64, _c_p, _c_i64,                     # k, k stride, v, v stride
+        _c_p, _c_p, _c_i64,                             # cos, sin, cos/sin stride
+        _c_p, _c_i64,                                   # cache, NB
+        _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
+        _c_p, _c_i32,                                   # ctx, B
+        _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # H, Hkv, D, bs, dtype
+        _c_f32, _c_i32,                                 # scale, partition
+        _c_p, _c_sz, _c_p,                              # workspace, bytes, stream
+    ]),
     "ndl_varlen_prefill": (_c_i32, [
         _c_p, _c_p, _c_i64,                             # out, q, q stride
         _c_p, _c_i64,                                   # cache, NB
@@ -92,6 +105,11 @@ _SIGNATURES = {
         _c_p, _c_p, _c_i32, _c_i64, _c_i32, _c_i32,     # cu, ctx, B, T, max_seqlen, max_ctx
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # H, Hkv, D, bs, dtype
         _c_f32, _c_p,                                   # scale, stream
+    ]),
+    "ndl_kv_block_copy": (_c_i32, [
+        _c_p, _c_i64, _c_p, _c_i64,                     # dst pools, dst NB, src pools, src NB
+        _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # layers, Hkv, bs, D, dtype
+        _c_p, _c_p, _c_i32, _c_p,                       # src ids, dst ids, pairs, stream
     ]),
 }
 

@@ -90,6 +90,11 @@ struct DecodeArgs {
   const u16* k_new;
   const u16* v_new;
   int64_t k_new_stride, v_new_stride;
+  // Rotary embedding of the step (null: q and k_new are already rotated): cos/sin rows of
+  // each sequence's new token, [seq][D] with row stride rope_stride.
+  const u16* rope_cos;
+  const u16* rope_sin;
+  int64_t rope_stride;
 };
 
 __device__ __forceinline__ int64_t attended_len(const DecodeArgs& a, int seq) {
@@ -164,9 +169,10 @@ __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
 // the sequence (C = ceil(n / NW)) and the waves combine through LDS.
 // Two waves per SIMD for the default two-deep stream kernel (its 256-register budget), so
 // that the fused append's few extra registers do not halve its occupancy.
-template <int D, int NBUF, int NW, bool APP>
+template <int D, int NBUF, int NW, bool APP, bool ROPE = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     NW == 1 && NBUF == 2 ? 2 : 1))) void paged_decode_kernel(DecodeArgs a) {
+  static_assert(APP || !ROPE, "the rotary form is a form of the fused append");
   constexpr int KS = D / 32;   // k-steps of the QK^T MFMA
   constexpr int DPL = D / 16;  // head_dim elements per lane per V row
   constexpr int E = 4 * DPL;   // accumulator elements per lane (head_dim E*j .. + E of head c)
@@ -254,6 +260,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         qb[s] = __builtin_bit_cast(bf16x8, w);
       }
     }
+    if constexpr (ROPE) {
+      // RoPE of q (attention.py:88, :277-283): the lane's element d = 32 s + 8 j + e pairs
+      // with d + D/2, which is the same lane's chunk s + KS/2.
+      const u16* crow = a.rope_cos + (int64_t)seq * a.rope_stride + 8 * j;
+      const u16* srow = a.rope_sin + (int64_t)seq * a.rope_stride + 8 * j;
+#pragma unroll
+      for (int s = 0; s < KS / 2; ++s) {
+        u32x4 lo, hi;
+        rope8(__builtin_bit_cast(u32x4, qb[s]), __builtin_bit_cast(u32x4, qb[s + KS / 2]),
+              ld16(crow + 32 * s), ld16(crow + 32 * (s + KS / 2)), ld16(srow + 32 * s),
+              ld16(srow + 32 * (s + KS / 2)), lo, hi);
+        qb[s] = __builtin_bit_cast(bf16x8, lo);
+        qb[s + KS / 2] = __builtin_bit_cast(bf16x8, hi);
+      }
+    }
     const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
 
     // Fused append (attention.py:141-154 before :156-159): the new token of the step sits
@@ -271,7 +292,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     VT v_app = {};
     int64_t app_blk = -1;   // the last tile's block (its table column), if valid
     if (app) {
-      k_app = ld16(a.k_new + (int64_t)seq * a.k_new_stride + (int64_t)kvh * D + 8 * k_chunk);
+      const u16* krow = a.k_new + (int64_t)seq * a.k_new_stride + (int64_t)kvh * D;
+      k_app = ld16(krow + 8 * k_chunk);
+      if constexpr (ROPE) {
+        // RoPE of the new key row: chunk k_chunk pairs with chunk k_chunk ^ CPR/2
+        constexpr int HC = CPR / 2;
+        const bool first_half = k_chunk < HC;
+        const int lo_c = first_half ? k_chunk : k_chunk - HC;
+        const u32x4 partner = ld16(krow + 8 * (k_chunk ^ HC));
+        const u16* crow = a.rope_cos + (int64_t)seq * a.rope_stride + 8 * lo_c;
+        const u16* srow = a.rope_sin + (int64_t)seq * a.rope_stride + 8 * lo_c;
+        u32x4 lo, hi;
+        rope8(first_half ? k_app : partner, first_half ? partner : k_app, ld16(crow),
+              ld16(crow + 8 * HC), ld16(srow), ld16(srow + 8 * HC), lo, hi);
+        k_app = first_half ? lo : hi;
+      }
       v_app = load_vrow<D>(a.v_new + (int64_t)seq * a.v_new_stride + (int64_t)kvh * D + DPL * c);
       if constexpr (kStoreRow) {
         const int64_t b = a.block_table[(int64_t)seq * a.bt_row_stride + n_tiles - 1];
@@ -557,11 +592,24 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
       if (b >= 0 && b < a.num_blocks) {
         const bool is_v = lane >= CH;
         const int ch = is_v ? lane - CH : lane;
-        const u16* src = (is_v ? a.v_new + (int64_t)seq * a.v_new_stride
-                               : a.k_new + (int64_t)seq * a.k_new_stride) + (int64_t)kvh * D + 8 * ch;
+        const u16* src_row = (is_v ? a.v_new + (int64_t)seq * a.v_new_stride
+                                   : a.k_new + (int64_t)seq * a.k_new_stride) + (int64_t)kvh * D;
         u16* row = const_cast<u16*>(is_v ? a.vplane : a.kplane) +
                    (b * a.num_kv_heads + kvh) * (int64_t)(16 * D) + (ctx & 15) * D + 8 * ch;
-        st16(row, ld16(src));
+        u32x4 val = ld16(src_row + 8 * ch);
+        if (!is_v && a.rope_cos != nullptr) {   // the key row rotated as the attention did
+          constexpr int HC = CH / 2;
+          const bool first_half = ch < HC;
+          const int lo_c = first_half ? ch : ch - HC;
+          const u32x4 partner = ld16(src_row + 8 * (ch ^ HC));
+          const u16* crow = a.rope_cos + (int64_t)seq * a.rope_stride + 8 * lo_c;
+          const u16* srow = a.rope_sin + (int64_t)seq * a.rope_stride + 8 * lo_c;
+          u32x4 lo, hi;
+          rope8(first_half ? val : partner, first_half ? partner : val, ld16(crow),
+                ld16(crow + 8 * HC), ld16(srow), ld16(srow + 8 * HC), lo, hi);
+          val = first_half ? lo : hi;
+        }
+        st16(row, val);
       }
     }
   }
@@ -669,13 +717,30 @@ inline int64_t decode_resident_waves(const void* fn, int block = 64) {
 
 // APP: with the fused append (a separate instantiation, so that the attention-only kernel
 // carries none of its registers).
-template <int D, bool APP = false> const void* decode_kernel_fn(int depth) {
-  return depth == 2 ? (const void*)paged_decode_kernel<D, 2, 1, APP>
-                    : depth == 4 ? (const void*)paged_decode_kernel<D, 4, 1, APP>
-                                 : (const void*)paged_decode_kernel<D, 3, 1, APP>;
+template <int D, bool APP = false, bool ROPE = false> const void* decode_kernel_fn(int depth) {
+  return depth == 2 ? (const void*)paged_decode_kernel<D, 2, 1, APP, ROPE>
+                    : depth == 4 ? (const void*)paged_decode_kernel<D, 4, 1, APP, ROPE>
+                                 : (const void*)paged_decode_kernel<D, 3, 1, APP, ROPE>;
 }
-template <int D, bool APP = false> const void* seq_split_kernel_fn() {
-  return (const void*)paged_decode_kernel<D, 2, seq_split_waves<D>(), APP>;
+template <int D, bool APP = false, bool ROPE = false> const void* seq_split_kernel_fn() {
+  return (const void*)paged_decode_kernel<D, 2, seq_split_waves<D>(), APP, ROPE>;
+}
+
+// The attention kernel for one call: head_dim, fused append, rotary form, split.
+inline const void* pick_decode_kernel(int head_dim, bool app, bool rope, bool seq_split,
+                                      int depth) {
+  if (seq_split) {
+    if (head_dim == 128)
+      return rope ? seq_split_kernel_fn<128, true, true>()
+                  : app ? seq_split_kernel_fn<128, true>() : seq_split_kernel_fn<128>();
+    return rope ? seq_split_kernel_fn<64, true, true>()
+                : app ? seq_split_kernel_fn<64, true>() : seq_split_kernel_fn<64>();
+  }
+  if (head_dim == 128)
+    return rope ? decode_kernel_fn<128, true, true>(depth)
+                : app ? decode_kernel_fn<128, true>(depth) : decode_kernel_fn<128>(depth);
+  return rope ? decode_kernel_fn<64, true, true>(depth)
+              : app ? decode_kernel_fn<64, true>(depth) : decode_kernel_fn<64>(depth);
 }
 
 struct DecodeLayout {
@@ -805,7 +870,8 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
                          float scale, int partition_tokens, void* workspace,
                          size_t workspace_bytes, const void* k_new, int64_t k_new_stride,
                          const void* v_new, int64_t v_new_stride, ndl_stream_t stream,
-                         bool static_scratch = false) {
+                         bool static_scratch = false, const void* rope_cos = nullptr,
+                         const void* rope_sin = nullptr, int64_t rope_stride = 0) {
   if (dtype != NDL_DTYPE_BF16) return NDL_ERR_UNSUPPORTED;
   if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -866,25 +932,24 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   a.v_new = (const u16*)v_new;
   a.k_new_stride = k_new_stride;
   a.v_new_stride = v_new_stride;
+  a.rope_cos = (const u16*)rope_cos;
+  a.rope_sin = (const u16*)rope_sin;
+  a.rope_stride = rope_stride;
 
   hipStream_t s = (hipStream_t)stream;
   const dim3 grid((unsigned)grid_waves);
   const bool app = k_new != nullptr;
+  const bool rope = rope_cos != nullptr;
   void* args[] = {&a};
   if (lay.seq_split) {  // one workgroup per (kv head, sequence), kv head fastest
-    const void* fn = head_dim == 128
-                         ? (app ? seq_split_kernel_fn<128, true>() : seq_split_kernel_fn<128>())
-                         : (app ? seq_split_kernel_fn<64, true>() : seq_split_kernel_fn<64>());
+    const void* fn = pick_decode_kernel(head_dim, app, rope, true, 2);
     if (hipLaunchKernel(fn, grid, dim3(64 * lay.seq_split), args, 0, s) != hipSuccess) {
       (void)hipGetLastError();
       return NDL_ERR_LAUNCH;
     }
     return check_launch();
   }
-  const int depth = decode_pipeline_depth();
-  const void* fn = head_dim == 128
-                       ? (app ? decode_kernel_fn<128, true>(depth) : decode_kernel_fn<128>(depth))
-                       : (app ? decode_kernel_fn<64, true>(depth) : decode_kernel_fn<64>(depth));
+  const void* fn = pick_decode_kernel(head_dim, app, rope, false, decode_pipeline_depth());
   if (hipLaunchKernel(fn, grid, dim3(64), args, 0, s) != hipSuccess) {
     (void)hipGetLastError();
     return NDL_ERR_LAUNCH;
@@ -925,9 +990,15 @@ static int launch_decode_append(void* out, const void* q, int64_t q_tok_stride, 
                                 int num_kv_heads, int head_dim, int block_size, int dtype,
                                 float scale, int partition_tokens, void* workspace,
                                 size_t workspace_bytes, ndl_stream_t stream,
-                                bool static_scratch) {
+                                bool static_scratch, const void* rope_cos = nullptr,
+                                const void* rope_sin = nullptr, int64_t rope_stride = 0) {
   if (num_seqs > 0) {
     if (!k || !v) return NDL_ERR_INVALID_ARG;
+    if (rope_cos != nullptr || rope_sin != nullptr) {
+      if (!rope_cos || !rope_sin || rope_stride < head_dim || (rope_stride & 7) ||
+          (((uintptr_t)rope_cos | (uintptr_t)rope_sin) & 15u))
+        return NDL_ERR_INVALID_ARG;
+    }
     if (((uintptr_t)k | (uintptr_t)v) & 15u) return NDL_ERR_INVALID_ARG;
     if (k_tok_stride < (int64_t)num_kv_heads * head_dim ||
         v_tok_stride < (int64_t)num_kv_heads * head_dim || ((k_tok_stride | v_tok_stride) & 7))
@@ -937,7 +1008,7 @@ static int launch_decode_append(void* out, const void* q, int64_t q_tok_stride, 
                        max_blocks_per_seq, context_lens, num_seqs, num_heads, num_kv_heads,
                        head_dim, block_size, dtype, scale, partition_tokens, workspace,
                        workspace_bytes, k, k_tok_stride, v, v_tok_stride, stream,
-                       static_scratch);
+                       static_scratch, rope_cos, rope_sin, rope_stride);
 }
 
 }  // namespace ndl
@@ -970,4 +1041,21 @@ extern "C" int ndl_paged_decode_append_noalloc(
                                    max_blocks_per_seq, context_lens, num_seqs, num_heads,
                                    num_kv_heads, head_dim, block_size, dtype, scale,
                                    partition_tokens, nullptr, 0, stream, true);
+}
+
+// RoPE of q and the new key row folded into the fused decode (see above).
+extern "C" int ndl_rope_paged_decode_append(
+    void* out, const void* q, int64_t q_tok_stride, const void* k, int64_t k_tok_stride,
+    const void* v, int64_t v_tok_stride, const void* cos, const void* sin,
+    int64_t cs_tok_stride, void* kv_cache, int64_t num_blocks, const int32_t* block_table,
+    int64_t bt_row_stride, int max_blocks_per_seq, const int32_t* context_lens, int num_seqs,
+    int num_heads, int num_kv_heads, int head_dim, int block_size, int dtype, float scale,
+    int partition_tokens, void* workspace, size_t workspace_bytes, ndl_stream_t stream) {
+  if (num_seqs > 0 && (cos == nullptr || sin == nullptr)) return NDL_ERR_INVALID_ARG;
+  return ndl::launch_decode_append(out, q, q_tok_stride, k, k_tok_stride, v, v_tok_stride,
+                                   kv_cache, num_blocks, block_table, bt_row_stride,
+                                   max_blocks_per_seq, context_lens, num_seqs, num_heads,
+                                   num_kv_heads, head_dim, block_size, dtype, scale,
+                                   partition_tokens, workspace, workspace_bytes, stream, false,
+                                   cos, sin, cs_tok_stride);
 }

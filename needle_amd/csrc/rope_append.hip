@@ -26,34 +26,6 @@ __device__ __forceinline__ int seq_of_token_rope(const int32_t* __restrict__ cu,
   return lo;
 }
 
-__device__ __forceinline__ float round_bf16(float x) {
-  return __uint_as_float(f32_to_bf16_bits(x) << 16);
-}
-
-// 8 bf16 of x[d..d+8) and x[d+D/2..d+D/2+8) -> rotated halves.
-__device__ __forceinline__ void rope8(const u32x4& lo, const u32x4& hi, const u32x4& clo,
-                                      const u32x4& chi, const u32x4& slo, const u32x4& shi,
-                                      u32x4& out_lo, u32x4& out_hi) {
-#pragma unroll
-  for (int w = 0; w < 4; ++w) {
-    float a[2], b[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float xl = h ? bf16_hi(lo[w]) : bf16_lo(lo[w]);
-      const float xh = h ? bf16_hi(hi[w]) : bf16_lo(hi[w]);
-      const float cl = h ? bf16_hi(clo[w]) : bf16_lo(clo[w]);
-      const float ch = h ? bf16_hi(chi[w]) : bf16_lo(chi[w]);
-      const float sl = h ? bf16_hi(slo[w]) : bf16_lo(slo[w]);
-      const float sh = h ? bf16_hi(shi[w]) : bf16_lo(shi[w]);
-      // first half: x*cos + (-x_hi)*sin ; second half: x_hi*cos + x*sin
-      a[h] = round_bf16(xl * cl) + round_bf16(-xh * sl);
-      b[h] = round_bf16(xh * ch) + round_bf16(xl * sh);
-    }
-    out_lo[w] = pack_bf16x2(a[0], a[1]);
-    out_hi[w] = pack_bf16x2(b[0], b[1]);
-  }
-}
-
 struct RopeArgs {
   u16* q_out;
   const u16* q;

@@ -3,12 +3,14 @@
 Same constructor, the same forward() signature and meaning
 (attention.py:36-96), the same parameter names (q_proj/k_proj/v_proj/o_proj),
 and the same KV pool layout [2, num_blocks, num_kv_heads, block_size,
-head_dim].  Projections stay torch GEMMs (attention.py:84-86).  RoPE
-(attention.py:88, 277-288) and the K/V append run as one HIP launch
-(ndl_rope_kv_append, bit-exact with the reference's bf16 rounding), then:
+head_dim].  Projections stay torch GEMMs (attention.py:84-86).  The rest of
+forward is, bit-exact with the reference's bf16 rounding of RoPE (attention.py:88,
+277-288):
 
-  prefill (attention.py:102-107): ndl_varlen_prefill
-  decode  (attention.py:140-159): ndl_paged_decode
+  prefill (attention.py:88, 102-107): ndl_rope_kv_append (RoPE of q and k, the append of
+          k and v), then ndl_varlen_prefill
+  decode  (attention.py:88, 140-159): ndl_rope_paged_decode_append, one launch for RoPE,
+          the append and the attention (plus the merge launch of the stream split)
 
 The reference's two seams stay available with their own signatures, taking
 q and k already rotated, for callers that apply RoPE themselves
@@ -68,7 +70,9 @@ class Attention(nn.Module):
         self.k_proj = nn.Linear(hidden, self.num_kv_heads * self.head_dim, bias=qkv_bias)
         self.v_proj = nn.Linear(hidden, self.num_kv_heads * self.head_dim, bias=qkv_bias)
         self.o_proj = nn.Linear(self.num_heads * self.head_dim, hidden, bias=False)
-        self._workspace = None
+        # Decode workspaces, newest last.  A grown workspace never frees the older ones: a
+        # HIP graph captured with an older one keeps writing it on every replay.
+        self._workspaces = []
         self.fuse_rope = True
 
     def forward(self, hidden_states: torch.Tensor, positions: torch.Tensor,
@@ -80,13 +84,14 @@ class Attention(nn.Module):
         k = self.k_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
         v = self.v_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
         if self.fuse_rope:
-            q = ops.rope_kv_append(q, k, v, cos, sin, kv_cache, block_table, context_lens,
-                                   cu_seqlens if is_prefill else None)
             if is_prefill:
+                q = ops.rope_kv_append(q, k, v, cos, sin, kv_cache, block_table, context_lens,
+                                       cu_seqlens)
                 out = self._prefill_attend(q, kv_cache, block_table, cu_seqlens, context_lens,
                                            max_seqlen)
             else:
-                out = self._decode_attend(q, kv_cache, block_table, context_lens)
+                out = self._decode_attend(q, kv_cache, block_table, context_lens, new_k=k,
+                                          new_v=v, cos=cos, sin=sin)
         else:
             q, k = apply_rope(q, k, cos, sin)
             if is_prefill:
@@ -109,12 +114,14 @@ class Attention(nn.Module):
     def _decode(self, q, k, v, kv_cache, block_table, context_lens):
         return self._decode_attend(q, kv_cache, block_table, context_lens, new_k=k, new_v=v)
 
-    def _decode_attend(self, q, kv_cache, block_table, context_lens, new_k=None, new_v=None):
+    def _decode_attend(self, q, kv_cache, block_table, context_lens, new_k=None, new_v=None,
+                       cos=None, sin=None):
         need = ops.decode_workspace_bytes(q.shape[0], self.num_heads, self.num_kv_heads,
                                           self.head_dim, block_table.shape[1], kv_cache.shape[3])
-        ws = self._workspace
+        ws = self._workspaces[-1] if self._workspaces else None
         if ws is None or ws.numel() < need or ws.device != q.device:
-            ws = self._workspace = ops.decode_workspace(need, q.device)
+            ws = ops.decode_workspace(need, q.device)
+            self._workspaces.append(ws)
         return ops.paged_decode(q, kv_cache, block_table, context_lens, self.scale,
                                 self.num_heads, self.num_kv_heads, self.head_dim,
-                                workspace=ws, new_k=new_k, new_v=new_v)
+                                workspace=ws, new_k=new_k, new_v=new_v, cos=cos, sin=sin)

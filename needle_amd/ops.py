@@ -196,7 +196,9 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
                  out: Optional[torch.Tensor] = None,
                  workspace: Optional[torch.Tensor] = None,
                  new_k: Optional[torch.Tensor] = None,
-                 new_v: Optional[torch.Tensor] = None) -> torch.Tensor:
+                 new_v: Optional[torch.Tensor] = None,
+                 cos: Optional[torch.Tensor] = None,
+                 sin: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Paged decode attention; same signature as _decode_pytorch (attention.py:291).
 
     Sequence i attends min(context_lens[i] + 1, W * block_size) cached tokens.
@@ -208,6 +210,10 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
     (attention.py:141-154) done in the same launch, with the same cache bytes and output as
     kv_append followed by paged_decode.  Requires that no two sequences attend the same
     block (as BlockAllocator's tables guarantee).
+
+    cos / sin ([num_seqs, head_dim], with new_k / new_v): q and new_k are the projections'
+    outputs, not yet rotated; the launch applies the rotary embedding of attention.py:88 to
+    both first (bit-identical to rope_kv_append followed by paged_decode).
     """
     _check_cache(kv_cache)
     dev = kv_cache.device
@@ -238,6 +244,7 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
     if workspace is None or workspace.numel() * workspace.element_size() < need:
         workspace = decode_workspace(need, dev)
     if new_k is None and new_v is None:
+        _require(cos is None and sin is None, "cos / sin need new_k / new_v")
         rc = lib.ndl_paged_decode(
             out.data_ptr(), q.data_ptr(), qs, kv_cache.data_ptr(), num_blocks,
             block_table.data_ptr(), block_table.stride(0), w,
@@ -252,6 +259,24 @@ def paged_decode(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Ten
         _require(x.shape[0] == n_seqs, f"{name} must have one row per sequence")
     ks = _rows("new_k", new_k, num_kv_heads, head_dim, dev)
     vs = _rows("new_v", new_v, num_kv_heads, head_dim, dev)
+    if cos is not None or sin is not None:
+        _require(cos is not None and sin is not None, "cos and sin go together")
+        for name, x in (("cos", cos), ("sin", sin)):
+            _require(x.dtype == kv_cache.dtype, f"{name} dtype must match kv_cache", TypeError)
+            _require(x.dim() == 2 and x.shape[0] == n_seqs and x.shape[1] == head_dim,
+                     f"{name} must be [{n_seqs}, {head_dim}], got {tuple(x.shape)}")
+            _require(x.device == dev and x.stride(1) == 1, f"{name} rows must be contiguous")
+        _require(cos.stride(0) == sin.stride(0) or n_seqs <= 1, "cos and sin strides differ")
+        cs = cos.stride(0) if n_seqs > 1 else head_dim
+        rc = lib.ndl_rope_paged_decode_append(
+            out.data_ptr(), q.data_ptr(), qs, new_k.data_ptr(), ks, new_v.data_ptr(), vs,
+            cos.data_ptr(), sin.data_ptr(), cs,
+            kv_cache.data_ptr(), num_blocks, block_table.data_ptr(), block_table.stride(0), w,
+            context_lens.data_ptr(), n_seqs, num_heads, num_kv_heads, head_dim, bs,
+            _DTYPES[q.dtype], float(scale), partition_tokens, workspace.data_ptr(), need,
+            _stream(dev))
+        _lib.check(rc, "ndl_rope_paged_decode_append")
+        return out
     rc = lib.ndl_paged_decode_append(
         out.data_ptr(), q.data_ptr(), qs, new_k.data_ptr(), ks, new_v.data_ptr(), vs,
         kv_cache.data_ptr(), num_blocks, block_table.data_ptr(), block_table.stride(0), w,
@@ -308,3 +333,56 @@ def varlen_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.T
         float(scale), _stream(dev))
     _lib.check(rc, "ndl_varlen_prefill")
     return out
+
+
+def kv_block_copy(dst_pools, src_pools, src_ids: torch.Tensor, dst_ids: torch.Tensor) -> None:
+    """Copy block src_ids[j] to block dst_ids[j] in every layer's pool, both planes, in one
+    launch (the KV swap copies; the reference copies per layer and block,
+    runner.py:175-192).
+
+    dst_pools / src_pools: equal-length lists of [2, NB, Hkv, bs, D] tensors, each on the GPU
+    or in pinned CPU memory (pin_memory=True).  src_ids / dst_ids: int32 [pairs] on the GPU or
+    pinned.  Enqueued on the current stream of the GPU the pools (or ids) live on.
+    """
+    import ctypes
+    _require(len(dst_pools) == len(src_pools), "dst_pools and src_pools differ in length")
+    if not dst_pools:
+        return
+    ref = dst_pools[0]
+    _require(ref.dim() == 5 and ref.shape[0] == 2, "pools must be [2, NB, Hkv, bs, D]")
+    dev = next((t.device for t in list(dst_pools) + list(src_pools) + [src_ids, dst_ids]
+                if t.is_cuda), None)
+    _require(dev is not None, "at least one of the pools or ids must be on the GPU")
+
+    def check_pool(t, nb):
+        _require(t.dim() == 5 and tuple(t.shape[2:]) == tuple(ref.shape[2:]) and t.shape[0] == 2
+                 and t.shape[1] == nb, f"pool shape {tuple(t.shape)} differs from its set")
+        _require(t.dtype == ref.dtype and t.dtype in _DTYPES, "pools must share a 16-bit dtype",
+                 TypeError)
+        _require(t.is_contiguous(), "pools must be contiguous")
+        _require(t.device == dev or (t.device.type == "cpu" and t.is_pinned()),
+                 "a CPU pool must be pinned (pin_memory=True)")
+
+    dst_nb, src_nb = dst_pools[0].shape[1], src_pools[0].shape[1]
+    for t in dst_pools:
+        check_pool(t, dst_nb)
+    for t in src_pools:
+        check_pool(t, src_nb)
+    for name, t in (("src_ids", src_ids), ("dst_ids", dst_ids)):
+        _require(t.dtype == torch.int32 and t.dim() == 1 and t.is_contiguous(),
+                 f"{name} must be a contiguous int32 vector", TypeError)
+        _require(t.device == dev or (t.device.type == "cpu" and t.is_pinned()),
+                 f"{name} must be on {dev} or pinned")
+    _require(src_ids.numel() == dst_ids.numel(), "src_ids and dst_ids differ in length")
+    n = src_ids.numel()
+    if n == 0:
+        return
+    arr = ctypes.c_void_p * len(dst_pools)
+    dsts = arr(*[t.data_ptr() for t in dst_pools])
+    srcs = arr(*[t.data_ptr() for t in src_pools])
+    _, _, hkv, bs, d = ref.shape
+    lib = _lib.load()
+    rc = lib.ndl_kv_block_copy(dsts, dst_nb, srcs, src_nb, len(dst_pools), hkv, bs, d,
+                               _DTYPES[ref.dtype], src_ids.data_ptr(), dst_ids.data_ptr(), n,
+                               _stream(dev))
+    _lib.check(rc, "ndl_kv_block_copy")
