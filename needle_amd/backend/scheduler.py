@@ -1,114 +1,156 @@
-"""Continuous-batching scheduler (reference needle/backend/scheduler.py:22-154).
+"""Continuous-batching scheduler producing the block tables the paged kernels read.
 
-Same policy and defaults, step for step:
-  1. swap SWAPPED sequences back in when their blocks fit (:54-67);
-  2. admit WAITING sequences in FIFO order while the running count stays under
-     max_num_seqs, the summed length of running sequences stays within
-     max_num_batched_tokens and their blocks fit (:69-88);
-  3. while no GPU block is free, preempt the newest running sequence: swap it
-     out if the CPU pool can hold it, else free its blocks for recompute
-     (:90-109);
-  4. give every decoding sequence one more block when its length needs it (:111-118);
-  5. split running sequences into prefill and decode (:120-134).
-The only change: prefill/decode is decided by Sequence.prefilled (see
-sequence.py), so a recompute-preempted sequence is prefilled again.
+The policy is the reference's (needle/backend/scheduler.py:49-134), because it decides
+which block ids reach block_table; each step, in this order:
+
+  resume    swapped sequences, oldest first, each as soon as its whole block list fits
+            on the GPU (every swapped sequence is tried, not only the first);
+  admit     queued sequences in arrival order while the active count stays below
+            max_num_seqs, the summed length of the active sequences plus the newcomer
+            stays within max_num_batched_tokens, and its blocks fit;
+  evict     while the GPU pool has no free block, the most recently activated sequence
+            leaves: to the CPU pool when that can hold all its blocks, otherwise its
+            blocks are released and it goes back to the head of the queue;
+  extend    every sequence with ready K/V gets one more block when its length needs it
+            (when several need one and the pool runs dry, the newest sequences are evicted
+            by the rule above; the reference raises MemoryError there);
+  split     active sequences without ready K/V are prefilled, the others decode.
+
+So every table covers position length-1 (the slot a decode step appends to) and no
+block is shared between sequences.  A sequence evicted without a CPU copy is prefilled
+again when readmitted (see request.py).
 """
 from __future__ import annotations
 
 from collections import deque
-from typing import Dict, List
+from dataclasses import dataclass, field
+from typing import Deque, Dict, List
 
 from .block_allocator import BlockAllocator
-from .sequence import SchedulerOutput, Sequence, SequenceStatus
+from .request import Phase, SeqState
+
+
+@dataclass
+class StepPlan:
+    """One step's work: the two forward groups and the block copies that precede them."""
+    prefill: List[SeqState] = field(default_factory=list)
+    decode: List[SeqState] = field(default_factory=list)
+    swap_in: Dict[int, int] = field(default_factory=dict)    # CPU id -> GPU id
+    swap_out: Dict[int, int] = field(default_factory=dict)   # GPU id -> CPU id
+    released: List[int] = field(default_factory=list)        # GPU ids of evicted K/V
+
+    @property
+    def seqs(self) -> List[SeqState]:
+        return self.prefill + self.decode
+
+    @property
+    def empty(self) -> bool:
+        return not self.prefill and not self.decode
 
 
 class Scheduler:
-    def __init__(self, block_allocator: BlockAllocator, max_num_seqs: int = 256,
+    def __init__(self, allocator: BlockAllocator, max_num_seqs: int = 256,
                  max_num_batched_tokens: int = 8192):
-        self.allocator = block_allocator
+        self.allocator = allocator
+        self.block_size = allocator.block_size
         self.max_num_seqs = max_num_seqs
         self.max_num_batched_tokens = max_num_batched_tokens
-        self.waiting: deque = deque()
-        self.running: List[Sequence] = []
-        self.swapped: List[Sequence] = []
-        self._block_tables: Dict[int, List[int]] = {}
-        self._cpu_block_tables: Dict[int, List[int]] = {}
+        self.queue: Deque[SeqState] = deque()
+        self.active: List[SeqState] = []
+        self.swapped: List[SeqState] = []
 
-    def add_sequence(self, seq: Sequence) -> None:
-        self.waiting.append(seq)
+    def add(self, seq: SeqState) -> None:
+        seq.phase = Phase.QUEUED
+        self.queue.append(seq)
 
-    def schedule(self) -> SchedulerOutput:
-        swap_in_map: Dict[int, int] = {}
-        swap_out_map: Dict[int, int] = {}
-        blocks_to_free: List[int] = []
+    def pending(self) -> bool:
+        return bool(self.queue or self.active or self.swapped)
 
-        still_swapped: List[Sequence] = []
+    def schedule(self) -> StepPlan:
+        plan = StepPlan()
+        self._resume(plan)
+        self._admit()
+        self._evict(plan)
+        self._extend(plan)
+        for s in self.active:
+            (plan.decode if s.kv_ready else plan.prefill).append(s)
+        return plan
+
+    def finish(self, seq: SeqState) -> None:
+        """Return a finished sequence's blocks; calling it twice is harmless."""
+        if seq.phase is Phase.ACTIVE and seq.blocks:
+            self.allocator.free_gpu_blocks(seq.blocks)
+        elif seq.phase is Phase.SWAPPED and seq.blocks:
+            self.allocator.free_cpu_blocks(seq.blocks)
+        seq.blocks = []
+        for pool in (self.active, self.swapped):
+            if seq in pool:
+                pool.remove(seq)
+        if seq in self.queue:
+            self.queue.remove(seq)
+        seq.phase = Phase.DONE
+
+    # ---------------------------------------------------------------- policy steps
+
+    def _activate(self, seq: SeqState, blocks: List[int]) -> None:
+        seq.blocks = blocks
+        seq.phase = Phase.ACTIVE
+        self.active.append(seq)
+
+    def _resume(self, plan: StepPlan) -> None:
+        waiting_for_room = []
         for seq in self.swapped:
-            cpu_blocks = self._cpu_block_tables[seq.seq_id]
-            if self.allocator.can_allocate_gpu(len(cpu_blocks)):
-                mapping = self.allocator.swap_in(cpu_blocks)
-                swap_in_map.update(mapping)
-                self._block_tables[seq.seq_id] = [mapping[c] for c in cpu_blocks]
-                del self._cpu_block_tables[seq.seq_id]
-                seq.status = SequenceStatus.RUNNING
-                self.running.append(seq)
-            else:
-                still_swapped.append(seq)
-        self.swapped = still_swapped
+            if not self.allocator.can_allocate_gpu(len(seq.blocks)):
+                waiting_for_room.append(seq)
+                continue
+            moved = self.allocator.swap_in(seq.blocks)
+            plan.swap_in.update(moved)
+            self._activate(seq, [moved[c] for c in seq.blocks])
+        self.swapped = waiting_for_room
 
-        batched = sum(s.length for s in self.running)
-        while self.waiting:
-            seq = self.waiting[0]
-            need_blocks = seq.num_logical_blocks
-            if (len(self.running) >= self.max_num_seqs
-                    or batched + seq.length > self.max_num_batched_tokens
-                    or not self.allocator.can_allocate_gpu(need_blocks)):
+    def _admit(self) -> None:
+        in_flight = sum(s.length for s in self.active)
+        while self.queue and len(self.active) < self.max_num_seqs:
+            head = self.queue[0]
+            need = head.blocks_needed(self.block_size)
+            if in_flight + head.length > self.max_num_batched_tokens:
                 break
-            self.waiting.popleft()
-            self._block_tables[seq.seq_id] = self.allocator.allocate_gpu_blocks(need_blocks)
-            seq.status = SequenceStatus.RUNNING
-            self.running.append(seq)
-            batched += seq.length
+            if not self.allocator.can_allocate_gpu(need):
+                break
+            self.queue.popleft()
+            self._activate(head, self.allocator.allocate_gpu_blocks(need))
+            in_flight += head.length
 
-        while self.running and not self.allocator.can_allocate_gpu(1):
-            victim = self.running.pop()
-            gpu_blocks = self._block_tables.pop(victim.seq_id)
-            if self.allocator.num_free_cpu_blocks >= len(gpu_blocks):
-                mapping = self.allocator.swap_out(gpu_blocks)
-                swap_out_map.update(mapping)
-                self._cpu_block_tables[victim.seq_id] = [mapping[g] for g in gpu_blocks]
-                victim.status = SequenceStatus.SWAPPED
-                self.swapped.append(victim)
-            else:
-                self.allocator.free_gpu_blocks(gpu_blocks)
-                blocks_to_free.extend(gpu_blocks)
-                victim.status = SequenceStatus.WAITING
-                victim.prefilled = False            # its KV is gone: prefill again
-                self.waiting.appendleft(victim)
+    def _evict(self, plan: StepPlan) -> None:
+        while self.active and not self.allocator.can_allocate_gpu(1):
+            self._evict_newest(plan)
 
-        for seq in self.running:
-            if seq.prefilled:
-                table = self._block_tables[seq.seq_id]
-                if seq.num_logical_blocks > len(table):
-                    table.append(self.allocator.allocate_gpu())
+    def _evict_newest(self, plan: StepPlan) -> None:
+        seq = self.active.pop()
+        if self.allocator.num_free_cpu_blocks >= len(seq.blocks):
+            moved = self.allocator.swap_out(seq.blocks)
+            plan.swap_out.update(moved)
+            seq.blocks = [moved[g] for g in seq.blocks]
+            seq.phase = Phase.SWAPPED
+            self.swapped.append(seq)
+        else:
+            self.allocator.free_gpu_blocks(seq.blocks)
+            plan.released.extend(seq.blocks)
+            seq.blocks = []
+            seq.kv_ready = False
+            seq.phase = Phase.QUEUED
+            self.queue.appendleft(seq)
 
-        prefill = [s for s in self.running if not s.prefilled]
-        decode = [s for s in self.running if s.prefilled]
-        return SchedulerOutput(prefill_seqs=prefill, decode_seqs=decode,
-                               block_tables={k: list(v) for k, v in self._block_tables.items()},
-                               swap_in_map=swap_in_map, swap_out_map=swap_out_map,
-                               blocks_to_free=blocks_to_free)
-
-    def free_sequence(self, seq: Sequence) -> None:
-        if seq.seq_id in self._block_tables:
-            self.allocator.free_gpu_blocks(self._block_tables.pop(seq.seq_id))
-        if seq.seq_id in self._cpu_block_tables:
-            self.allocator.free_cpu_blocks(self._cpu_block_tables.pop(seq.seq_id))
-        seq.finish()
-        try:
-            self.running.remove(seq)
-        except ValueError:
-            pass
-
-    def has_unfinished_seqs(self) -> bool:
-        return bool(self.waiting or self.running or self.swapped)
+    def _extend(self, plan: StepPlan) -> None:
+        for seq in list(self.active):
+            if seq.phase is not Phase.ACTIVE:        # evicted below for an earlier one
+                continue
+            if not (seq.kv_ready and seq.blocks_needed(self.block_size) > len(seq.blocks)):
+                continue
+            # Several sequences can cross a block edge in one step while the eviction step
+            # left one free block; the reference then raises MemoryError.  Here the newest
+            # sequences are evicted, by the same rule, until the block fits.
+            while self.active and not self.allocator.can_allocate_gpu(1):
+                self._evict_newest(plan)
+            if seq.phase is Phase.ACTIVE:
+                seq.blocks.append(self.allocator.allocate_gpu())

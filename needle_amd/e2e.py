@@ -15,7 +15,7 @@ from typing import Optional
 import numpy as np
 
 from .backend.engine import LLMEngine
-from .backend.sequence import SamplingParams
+from .backend.request import SamplingParams
 from .model.config import QWEN2_0_5B, ModelConfig
 
 E2E_SEED = 1004
@@ -57,3 +57,27 @@ def run(engine: LLMEngine, reqs, sync=None, time_limit_s: Optional[float] = None
     if sync is not None:
         sync()
     return n_tok, time.perf_counter() - t0, finished
+
+
+def main(argv=None) -> None:
+    """python -m needle_amd.e2e [--requests N]: the benchmark's first N requests on cuda:0,
+    printing output tok/s (the command the kernel-trace profiles of this run use)."""
+    import argparse
+
+    import torch
+
+    p = argparse.ArgumentParser(description=main.__doc__.splitlines()[0])
+    p.add_argument("--requests", type=int, default=256)
+    p.add_argument("--time-limit", type=float, default=None)
+    args = p.parse_args(argv)
+    engine = build_engine()
+    reqs = requests(args.requests)
+    torch.cuda.synchronize()
+    n_tok, secs, finished = run(engine, reqs, sync=torch.cuda.synchronize,
+                                time_limit_s=args.time_limit)
+    print(f"e2e {len(reqs)} requests: {n_tok} tokens in {secs:.2f} s = {n_tok / secs:.1f} "
+          f"tok/s, {finished} finished", flush=True)
+
+
+if __name__ == "__main__":
+    main()

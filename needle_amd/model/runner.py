@@ -1,37 +1,176 @@
-"""ModelRunner: KV pools, batch metadata and one forward per step.
+"""ModelRunner: KV pools, batch metadata and the forwards of one engine step.
 
-Follows needle/model/runner.py:14-249 of the reference:
+Contract with the attention path (reference needle/model/runner.py:65-94, 194-249):
   * one KV pool per layer, [2, num_blocks, num_kv_heads, block_size, head_dim] in the
-    model dtype, zero-initialised (:65-78), plus an optional pinned CPU swap pool (:80-94);
-  * _prepare_inputs (:194-249): prefill feeds every token with context 0, decode the
-    last token with context length-1; positions ctx..ctx+n; cu_seqlens; block_table
-    padded with the dummy id num_blocks-1; max_seqlen from the host lists;
-  * a batch holding both prefill and decode sequences runs two forwards (:121-148).
-Differences:
-  * the metadata goes to the device in one pinned copy instead of five tensors;
-  * greedy sampling is one device argmax with one host copy for the whole batch
-    (the reference syncs once per sequence, sampler.py:24-29); non-greedy requests
-    use needle_amd.model.sampler;
-  * swapping copies all moved blocks of a layer with one gather and one scatter
-    (the reference copies one block at a time, runner.py:187-192);
-  * optionally, decode forwards replay HIP graphs captured per batch-size bucket
-    (enable_decode_graphs): the ~30 kernels of each layer launch from one graph
-    instead of one Python call each.  Rows beyond the live batch point at a
-    reserved scratch block that the allocator never hands out.
+    model dtype, zero-initialised, plus an optional pinned CPU pool for swapping;
+  * prefill feeds every token of a sequence with context 0, decode its newest token with
+    context length-1; positions ctx..ctx+n; cu_seqlens is the prefix sum of the token
+    counts; block_table rows are padded with num_blocks-1 to the widest row; a step with
+    both prefill and decode sequences runs two forwards.
+
+How this runner feeds the device:
+  * an eager batch goes to the device as one pinned int64 buffer (one copy, then views);
+  * decode steps can replay HIP graphs captured per batch-size bucket
+    (enable_decode_graphs).  Their metadata stays on the device between steps
+    (_DecodeRows): a sequence keeps its row for as long as it decodes, the step's
+    greedy tokens are written into the next step's input ids inside the graph, and the
+    host sends only what changed (context lengths, new rows, new blocks) as one small
+    scatter.  Padding rows point at a scratch block the allocator never hands out;
+  * greedy sampling is one device argmax and one host copy for the whole batch; other
+    rows go through needle_amd.model.sampler;
+  * swapping moves every block of every layer in one ndl_kv_block_copy launch per
+    direction (the reference issues one copy per layer and block, runner.py:175-192).
 """
 from __future__ import annotations
 
-from typing import List, Optional
+from dataclasses import dataclass
+from typing import Dict, List, Optional
 
+import numpy as np
 import torch
 
-from ..backend.sequence import ExecuteInput, ExecuteOutput, SchedulerOutput
+from .. import ops
+from ..backend.request import SeqState
+from ..backend.scheduler import StepPlan
 from .config import ModelConfig
 from .qwen2 import build_model, random_init_
 from .sampler import sample
 
 
+@dataclass
+class Batch:
+    """The metadata of one forward (the arguments of Attention.forward besides q/k/v)."""
+    input_ids: torch.Tensor
+    positions: torch.Tensor
+    cu_seqlens: torch.Tensor
+    max_seqlen: int
+    block_table: torch.Tensor
+    context_lens: torch.Tensor
+    is_prefill: bool
+
+
+class _DecodeRows:
+    """Device-resident metadata of the graph-replayed decode batch.
+
+    One int32 device buffer holds, per row r < capacity: the next input token, the
+    context length and the block-table row.  Row r belongs to one sequence for as long as
+    it keeps decoding; a leaving sequence's row is filled with the last row's sequence and
+    the last row is reset to padding (token 0, context 0, every entry the scratch block).
+    Every step the host sends (flat index, value) pairs for what changed and applies them
+    with one scatter: the context lengths of the live rows, the rows that were filled, the
+    block ids a sequence gained.  The tokens of greedy rows are written by the graph itself.
+    """
+
+    def __init__(self, capacity: int, width: int, scratch_block: int, device):
+        self.capacity, self.width, self.scratch = capacity, width, scratch_block
+        self.meta = torch.zeros(capacity * (2 + width), dtype=torch.int32, device=device)
+        self.tok = self.meta[:capacity]
+        self.ctx = self.meta[capacity:2 * capacity]
+        self.table = self.meta[2 * capacity:].view(capacity, width)
+        self.table.fill_(scratch_block)
+        self.rows: List[SeqState] = []
+        self.sent_blocks: List[int] = []     # table entries the device holds, per row
+        self.dirty: List[bool] = []          # row refilled: send all of it
+        self.tok_on_device: List[bool] = []  # the graph wrote this row's newest token
+        self._staging: List[torch.Tensor] = []
+        self._events = [None, None]
+        self._turn = 0
+        self._dev_pairs = torch.empty(0, dtype=torch.int32, device=device)
+
+    def fits(self, seqs: List[SeqState], block_size: int) -> bool:
+        return len(seqs) <= self.capacity and all(
+            len(s.blocks) <= self.width and s.length <= self.width * block_size for s in seqs)
+
+    def forget_tokens(self) -> None:
+        """The newest tokens did not come from a replay (an eager decode step ran)."""
+        self.tok_on_device = [False] * len(self.rows)
+
+    def sync(self, seqs: List[SeqState]) -> None:
+        """Make rows 0..len(seqs)-1 hold exactly `seqs` (in any order) on the device."""
+        live = {id(s) for s in seqs}
+        upd: Dict[int, int] = {}          # flat index -> value; a later write wins
+        cap, w = self.capacity, self.width
+        # leaving sequences: refill their rows from the end, reset each vacated last row
+        r = 0
+        while r < len(self.rows):
+            if id(self.rows[r]) in live:
+                r += 1
+                continue
+            last = len(self.rows) - 1
+            upd[last] = 0
+            upd[cap + last] = 0
+            base = 2 * cap + last * w
+            for j in range(self.sent_blocks[last]):
+                upd[base + j] = self.scratch
+            if r != last:
+                # row r keeps its own old entries on the device until the refill below
+                self.rows[r] = self.rows[last]
+                self.dirty[r] = True
+                self.tok_on_device[r] = False
+            self.rows.pop()
+            self.sent_blocks.pop()
+            self.dirty.pop()
+            self.tok_on_device.pop()
+        # arriving sequences take the rows after the last one (all padding on the device)
+        present = {id(s) for s in self.rows}
+        for s in seqs:
+            if id(s) not in present:
+                self.rows.append(s)
+                self.sent_blocks.append(0)
+                self.dirty.append(True)
+                self.tok_on_device.append(False)
+        for r, s in enumerate(self.rows):
+            base = 2 * cap + r * w
+            nb = len(s.blocks)
+            sent = self.sent_blocks[r]
+            if self.dirty[r]:
+                for j in range(nb, sent):              # the previous occupant's extra entries
+                    upd[base + j] = self.scratch
+                sent = 0
+                self.dirty[r] = False
+            for j in range(sent, nb):
+                upd[base + j] = s.blocks[j]
+            self.sent_blocks[r] = nb
+            upd[cap + r] = s.length - 1
+            if not (self.tok_on_device[r] and s.params.greedy):
+                upd[r] = s.last_token
+        self._scatter(list(upd.keys()), list(upd.values()))
+
+    def _scatter(self, idx: List[int], val: List[int]) -> None:
+        n = len(idx)
+        if n == 0:
+            return
+        if self.meta.device.type != "cuda":          # host-side model of the same updates
+            self.meta[torch.tensor(idx, dtype=torch.long)] = torch.tensor(val, dtype=torch.int32)
+            return
+        if 2 * n > self._dev_pairs.numel():
+            size = max(8192, 4 * n)
+            self._staging = [torch.empty(size, dtype=torch.int32).pin_memory()
+                             for _ in range(2)]
+            self._events = [None, None]
+            self._dev_pairs = torch.empty(size, dtype=torch.int32, device=self.meta.device)
+        t = self._turn
+        self._turn ^= 1
+        if self._events[t] is not None:
+            self._events[t].synchronize()        # the copy that last read this buffer
+        host = self._staging[t]
+        arr = host.numpy()
+        arr[:n] = idx
+        arr[n:2 * n] = val
+        dev = self._dev_pairs[:2 * n]
+        dev.copy_(host[:2 * n], non_blocking=True)
+        ev = torch.cuda.Event()
+        ev.record()
+        self._events[t] = ev
+        self.meta.index_put_((dev[:n].long(),), dev[n:2 * n])
+
+    def row_of(self) -> Dict[int, int]:
+        return {id(s): r for r, s in enumerate(self.rows)}
+
+
 class ModelRunner:
+    DEFAULT_BUCKETS = (1, 2, 4, 8, 12, 16, 24, 32, 48, 64, 96, 128, 192, 256)
+
     def __init__(self, model_config: ModelConfig, block_size: int = 16, dtype: str = "bfloat16",
                  device: str = "cuda:0", seed: int = 0, model: Optional[torch.nn.Module] = None):
         self.model_config = model_config
@@ -43,8 +182,10 @@ class ModelRunner:
         self.model = model.to(device=self.device, dtype=self.dtype).eval()
         self.kv_caches: List[torch.Tensor] = []
         self.cpu_kv_caches: List[torch.Tensor] = []
-        self._graphs = {}
-        self._graph_width = 0
+        self._graphs: Dict[int, tuple] = {}
+        self._rows: Optional[_DecodeRows] = None
+
+    # ------------------------------------------------------------------ pools
 
     def bytes_per_block(self) -> int:
         cfg = self.model_config
@@ -53,9 +194,10 @@ class ModelRunner:
 
     def profile_memory(self, gpu_memory_utilization: float = 0.90, max_gpu_blocks: int = 0,
                        cpu_swap_bytes: int = 0):
-        """runner.py:44-63: blocks that fit in the free device memory (optionally capped),
-        and a CPU swap pool of cpu_swap_bytes (the reference sizes it at half the GPU pool)."""
-        if self.device.type != "cuda":                       # runner.py:46-47
+        """Blocks that fit in this share of the free device memory (optionally capped), and
+        the CPU swap pool's blocks for cpu_swap_bytes (runner.py:44-63 sizes that pool at
+        half the GPU pool, ~128 GB of pinned memory on this GPU, so here the caller says)."""
+        if self.device.type != "cuda":
             return (max_gpu_blocks or 512), cpu_swap_bytes // self.bytes_per_block()
         free, _total = torch.cuda.mem_get_info(self.device)
         n = max(1, int(free * gpu_memory_utilization) // self.bytes_per_block())
@@ -74,133 +216,151 @@ class ModelRunner:
             self.cpu_kv_caches = [torch.zeros(cshape, dtype=self.dtype, pin_memory=True)
                                   for _ in range(cfg.num_hidden_layers)]
 
-    @torch.no_grad()
-    def execute(self, sched_out: SchedulerOutput) -> ExecuteOutput:
-        if sched_out.swap_out_map and self.cpu_kv_caches:
-            self._swap(sched_out.swap_out_map, to_cpu=True)
-        if sched_out.swap_in_map and self.cpu_kv_caches:
-            self._swap(sched_out.swap_in_map, to_cpu=False)
-        logits = []
-        groups = [g for g in (sched_out.prefill_seqs, sched_out.decode_seqs) if g]
-        for seqs in groups:
-            prefill = not seqs[0].prefilled
-            out = None if prefill or not self._graphs else \
-                self._graph_decode(seqs, sched_out.block_tables)
-            if out is None:
-                out = self.forward(self.prepare_inputs(seqs, sched_out.block_tables, prefill))
-            logits.append(out)
-        all_seqs = sched_out.prefill_seqs + sched_out.decode_seqs
-        logits = logits[0] if len(logits) == 1 else torch.cat(logits, dim=0)
-        tokens = sample(logits, [s.request.sampling_params for s in all_seqs])
-        for s in sched_out.prefill_seqs:
-            s.prefilled = True
-        return ExecuteOutput(seq_ids=[s.seq_id for s in all_seqs], next_token_ids=tokens)
-
-    # ------------------------------------------------------------------ decode graphs
-
-    DEFAULT_BUCKETS = (1, 2, 4, 8, 12, 16, 24, 32, 48, 64, 96, 128, 192, 256)
-
     @property
     def scratch_block(self) -> int:
-        """The last pool block: padding rows of captured decode batches write here.
-        The engine keeps it out of the allocator when graphs are enabled."""
+        """The last pool block: padding rows of captured decode batches read and write
+        here.  An engine with decode graphs keeps it out of the allocator."""
         return self.kv_caches[0].shape[1] - 1
 
+    # ------------------------------------------------------------------ one step
+
     @torch.no_grad()
-    def enable_decode_graphs(self, max_model_len: int, buckets=DEFAULT_BUCKETS) -> None:
-        """Capture one decode graph per batch bucket (largest first, so workspaces the
-        first capture sizes are never reallocated under a later graph)."""
-        bs = self.block_size
-        width = (max_model_len + bs - 1) // bs
-        bmax = max(buckets)
-        dev = self.device
-        self._graph_width = width
-        self._st_ids = torch.zeros(bmax, dtype=torch.int64, device=dev)
-        self._st_pos = torch.zeros(bmax, dtype=torch.int64, device=dev)
-        self._st_ctx = torch.zeros(bmax, dtype=torch.int32, device=dev)
-        self._st_bt = torch.full((bmax, width), self.scratch_block, dtype=torch.int32, device=dev)
-        self._st_cu = torch.arange(bmax + 1, dtype=torch.int32, device=dev)
-        pool = torch.cuda.graph_pool_handle()
-        for b in sorted(buckets, reverse=True):
-            args = (self._st_ids[:b], self._st_pos[:b], self.kv_caches, self._st_bt[:b],
-                    self._st_cu[:b + 1], self._st_ctx[:b], 1, False)
-            self.model(*args)                       # warm-up: sizes workspaces, loads kernels
-            torch.cuda.synchronize(dev)
-            g = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(g, pool=pool):
-                out = self.model(*args)
-            self._graphs[b] = (g, out)
-        torch.cuda.synchronize(dev)
+    def execute(self, plan: StepPlan) -> List[int]:
+        """Run one planned step; returns the next token of every sequence of plan.seqs."""
+        # swap-in before swap-out: a CPU block released by a swap-in can be taken by a
+        # swap-out of the same step, and a sequence swapped in can be evicted again
+        if plan.swap_in:
+            self.swap(plan.swap_in, to_cpu=False)
+        if plan.swap_out:
+            self.swap(plan.swap_out, to_cpu=True)
+        tokens: List[int] = []
+        if plan.prefill:
+            tokens += self._sample(plan.prefill, self.forward(self.prepare_inputs(
+                plan.prefill, is_prefill=True)))
+            for s in plan.prefill:
+                s.kv_ready = True
+        if plan.decode:
+            toks = self._graph_decode(plan.decode) if self._graphs else None
+            if toks is None:
+                toks = self._sample(plan.decode, self.forward(self.prepare_inputs(
+                    plan.decode, is_prefill=False)))
+                if self._rows is not None:
+                    self._rows.forget_tokens()
+            tokens += toks
+        return tokens
 
-    def _graph_decode(self, seqs, block_tables):
-        b = len(seqs)
-        bucket = next((k for k in sorted(self._graphs) if k >= b), None)
-        if bucket is None or any(s.length > self._graph_width * self.block_size for s in seqs):
-            return None
-        width, scratch = self._graph_width, self.scratch_block
-        ids = [s.last_token_id for s in seqs] + [0] * (bucket - b)
-        ctx = [s.length - 1 for s in seqs] + [0] * (bucket - b)
-        table: List[int] = []
-        for s in seqs:
-            row = block_tables.get(s.seq_id, [])
-            table.extend(row + [scratch] * (width - len(row)))
-        table.extend([scratch] * (width * (bucket - b)))
-        host = torch.tensor(ids + ctx + table, dtype=torch.int64).pin_memory()
-        dev = host.to(self.device, non_blocking=True)
-        self._st_ids[:bucket].copy_(dev[:bucket])
-        self._st_pos[:bucket].copy_(dev[bucket:2 * bucket])
-        self._st_ctx[:bucket].copy_(dev[bucket:2 * bucket])
-        self._st_bt[:bucket].copy_(dev[2 * bucket:].view(bucket, width))
-        g, out = self._graphs[bucket]
-        g.replay()
-        return out[:b]
+    def _sample(self, seqs: List[SeqState], logits: torch.Tensor) -> List[int]:
+        return sample(logits, [s.params for s in seqs])
 
-    def forward(self, inp: ExecuteInput) -> torch.Tensor:
-        return self.model(inp.input_ids, inp.position_ids, self.kv_caches, inp.block_table,
-                          inp.cu_seqlens, inp.context_lens, inp.max_seqlen, inp.is_prefill)
+    def forward(self, batch: Batch) -> torch.Tensor:
+        return self.model(batch.input_ids, batch.positions, self.kv_caches, batch.block_table,
+                          batch.cu_seqlens, batch.context_lens, batch.max_seqlen,
+                          batch.is_prefill)
 
-    def prepare_inputs(self, seqs, block_tables, is_prefill: bool) -> ExecuteInput:
+    def prepare_inputs(self, seqs: List[SeqState], is_prefill: bool) -> Batch:
         ids: List[int] = []
         pos: List[int] = []
         cu: List[int] = [0]
         ctx: List[int] = []
         for s in seqs:
             if is_prefill:
-                toks, c = s.token_ids, 0
+                toks, c = s.tokens, 0
             else:
-                toks, c = [s.last_token_id], s.length - 1
-            ids.extend(toks)
-            pos.extend(range(c, c + len(toks)))
+                toks, c = [s.last_token], s.length - 1
+            ids += toks
+            pos += range(c, c + len(toks))
             cu.append(cu[-1] + len(toks))
             ctx.append(c)
-        width = max((len(block_tables.get(s.seq_id, [])) for s in seqs), default=1) or 1
-        dummy = (self.kv_caches[0].shape[1] if self.kv_caches else 1) - 1
-        table: List[int] = []
-        for s in seqs:
-            row = block_tables.get(s.seq_id, [])
-            table.extend(row + [dummy] * (width - len(row)))
         n_tok, n_seq = len(ids), len(seqs)
-        # One pinned int64 staging buffer -> one host-to-device copy.
-        host = torch.tensor(ids + pos + cu + table + ctx, dtype=torch.int64)
+        width = max((len(s.blocks) for s in seqs), default=1) or 1
+        pad = (self.kv_caches[0].shape[1] if self.kv_caches else 1) - 1
+        host = np.full(2 * n_tok + (n_seq + 1) + n_seq * width + n_seq, pad, dtype=np.int64)
+        host[:n_tok] = ids
+        host[n_tok:2 * n_tok] = pos
+        o = 2 * n_tok
+        host[o:o + n_seq + 1] = cu
+        o += n_seq + 1
+        tab = host[o:o + n_seq * width].reshape(n_seq, width)
+        for i, s in enumerate(seqs):
+            tab[i, :len(s.blocks)] = s.blocks
+        o += n_seq * width
+        host[o:o + n_seq] = ctx
+        t = torch.from_numpy(host)
         if self.device.type == "cuda":
-            host = host.pin_memory()
-        dev = host.to(self.device, non_blocking=True)
-        o = 0
-        input_ids = dev[o:o + n_tok]; o += n_tok
-        positions = dev[o:o + n_tok]; o += n_tok
-        cu_t = dev[o:o + n_seq + 1].to(torch.int32); o += n_seq + 1
-        bt = dev[o:o + n_seq * width].to(torch.int32).view(n_seq, width); o += n_seq * width
-        ctx_t = dev[o:o + n_seq].to(torch.int32)
-        max_seqlen = max(cu[i + 1] - cu[i] for i in range(n_seq)) if n_seq else 1
-        return ExecuteInput(input_ids=input_ids, position_ids=positions, cu_seqlens=cu_t,
-                            max_seqlen=max_seqlen, block_table=bt, context_lens=ctx_t,
-                            is_prefill=is_prefill)
+            t = t.pin_memory()
+        dev = t.to(self.device, non_blocking=True)
+        o = 2 * n_tok
+        return Batch(input_ids=dev[:n_tok], positions=dev[n_tok:o],
+                     cu_seqlens=dev[o:o + n_seq + 1].to(torch.int32),
+                     max_seqlen=max(cu[i + 1] - cu[i] for i in range(n_seq)) if n_seq else 1,
+                     block_table=dev[o + n_seq + 1:o + n_seq + 1 + n_seq * width]
+                     .to(torch.int32).view(n_seq, width),
+                     context_lens=dev[o + n_seq + 1 + n_seq * width:].to(torch.int32),
+                     is_prefill=is_prefill)
 
-    def _swap(self, mapping: dict, to_cpu: bool) -> None:
-        src = torch.tensor(list(mapping.keys()), dtype=torch.long)
-        dst = torch.tensor(list(mapping.values()), dtype=torch.long)
-        for gpu, cpu in zip(self.kv_caches, self.cpu_kv_caches):
-            if to_cpu:
-                cpu[:, dst] = gpu[:, src.to(self.device)].cpu()
-            else:
-                gpu[:, dst.to(self.device)] = cpu[:, src].to(self.device)
+    # ------------------------------------------------------------------ decode graphs
+
+    @torch.no_grad()
+    def enable_decode_graphs(self, max_model_len: int, buckets=DEFAULT_BUCKETS) -> None:
+        """Capture one decode graph per batch bucket, largest first in one memory pool."""
+        width = -(-max_model_len // self.block_size)
+        cap = max(buckets)
+        rows = _DecodeRows(cap, width, self.scratch_block, self.device)
+        self._rows = rows
+        self._cu = torch.arange(cap + 1, dtype=torch.int32, device=self.device)
+        pool = torch.cuda.graph_pool_handle()
+        for b in sorted(buckets, reverse=True):
+            self._decode_body(b)                 # warm-up: loads kernels, sizes workspaces
+            torch.cuda.synchronize(self.device)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g, pool=pool):
+                logits = self._decode_body(b)
+            self._graphs[b] = (g, logits)
+        torch.cuda.synchronize(self.device)
+
+    def _decode_body(self, b: int) -> torch.Tensor:
+        """The captured decode step of the first b rows (the forward only: torch's argmax
+        over a vocabulary row can split into a multi-workgroup reduction that clears its
+        semaphores with a memset, which a graph must not record)."""
+        rows = self._rows
+        ctx = rows.ctx[:b]
+        return self.model(rows.tok[:b], ctx.long(), self.kv_caches, rows.table[:b],
+                          self._cu[:b + 1], ctx, 1, False)
+
+    def _graph_decode(self, seqs: List[SeqState]) -> Optional[List[int]]:
+        rows = self._rows
+        if not rows.fits(seqs, self.block_size):
+            return None
+        b = len(seqs)
+        bucket = next((k for k in sorted(self._graphs) if k >= b), None)
+        if bucket is None:
+            return None
+        rows.sync(seqs)
+        g, logits = self._graphs[bucket]
+        g.replay()
+        nxt = torch.argmax(logits[:b], dim=-1)
+        rows.tok[:b].copy_(nxt)                  # the next step's input ids stay on the device
+        greedy = nxt.tolist()                    # one host copy (row order)
+        where = rows.row_of()
+        order = [where[id(s)] for s in seqs]
+        out = [greedy[r] for r in order]
+        if not all(s.params.greedy for s in seqs):
+            picks = sample(logits[torch.tensor(order, device=self.device)],
+                           [s.params for s in seqs])
+            out = [t if s.params.greedy else p for s, t, p in zip(seqs, out, picks)]
+        for r in range(b):
+            rows.tok_on_device[r] = True
+        return out
+
+    # ------------------------------------------------------------------ swapping
+
+    def swap(self, mapping: Dict[int, int], to_cpu: bool) -> None:
+        """Copy the blocks of `mapping` (source id -> destination id) of every layer between
+        the GPU pools and the pinned CPU pools, in one launch."""
+        if not mapping or not self.cpu_kv_caches:
+            return
+        ids = torch.tensor([list(mapping.keys()), list(mapping.values())], dtype=torch.int32)
+        ids = ids.pin_memory().to(self.device, non_blocking=True)
+        src, dst = (self.kv_caches, self.cpu_kv_caches) if to_cpu else \
+            (self.cpu_kv_caches, self.kv_caches)
+        ops.kv_block_copy(dst, src, ids[0], ids[1])

@@ -13,7 +13,7 @@ from typing import List, Optional
 import torch
 import torch.nn.functional as F
 
-from ..backend.sequence import SamplingParams
+from ..backend.request import SamplingParams
 
 
 @torch.no_grad()

@@ -1,106 +1,125 @@
-"""BlockAllocator semantics: the reference's own assertions
-(tests/unit/test_block_allocator.py:11-87, with the import pointed at this
-package) plus the FIFO order and the fragmented-table generator."""
+"""BlockAllocator: the block-id contract the kernels consume (block_allocator.py:10-124).
+
+Semantics pinned here:
+  * ids come out of a FIFO free list: a fresh pool hands out 0, 1, 2, ... and a freed id
+    goes to the back of the line;
+  * a block leaves the free list with ref_count 1 and returns when it drops to 0;
+  * an empty pool raises MemoryError (single and multi-block requests; a multi-block
+    request that cannot be met takes nothing);
+  * freeing a block that is already free raises AssertionError;
+  * swap_out / swap_in move blocks between the pools and return source -> destination maps;
+plus the allocator-churned table generator used for the long-context workload.
+"""
+import random
+
 import pytest
 
 from needle_amd.backend.block_allocator import BlockAllocator
 from needle_amd import workloads as wl
 
 
-@pytest.fixture
-def allocator():
-    return BlockAllocator(num_gpu_blocks=8, num_cpu_blocks=4, block_size=16)
+def test_fresh_pool_hands_out_ids_in_order():
+    a = BlockAllocator(num_gpu_blocks=6, num_cpu_blocks=0, block_size=16)
+    assert [a.allocate_gpu() for _ in range(3)] == [0, 1, 2]
+    assert a.allocate_gpu_blocks(3) == [3, 4, 5]
+    assert a.num_free_gpu_blocks == 0 and not a.can_allocate_gpu(1)
 
 
-class TestAllocateFree:
-    def test_allocate_single(self, allocator):
-        bid = allocator.allocate_gpu()
-        assert 0 <= bid < 8
-        assert allocator.num_free_gpu_blocks == 7
-
-    def test_allocate_multiple(self, allocator):
-        blocks = allocator.allocate_gpu_blocks(4)
-        assert len(blocks) == 4 and len(set(blocks)) == 4
-        assert allocator.num_free_gpu_blocks == 4
-
-    def test_free_returns_to_pool(self, allocator):
-        bid = allocator.allocate_gpu()
-        allocator.free_gpu(bid)
-        assert allocator.num_free_gpu_blocks == 8
-
-    def test_free_double_raises(self, allocator):
-        bid = allocator.allocate_gpu()
-        allocator.free_gpu(bid)
-        with pytest.raises(AssertionError):
-            allocator.free_gpu(bid)
-
-    def test_oom_raises(self, allocator):
-        allocator.allocate_gpu_blocks(8)
-        with pytest.raises(MemoryError):
-            allocator.allocate_gpu()
-        with pytest.raises(MemoryError):
-            allocator.allocate_gpu_blocks(1)
-
-    def test_can_allocate_check(self, allocator):
-        assert allocator.can_allocate_gpu(8)
-        assert not allocator.can_allocate_gpu(9)
+def test_freed_ids_queue_behind_the_never_used_ones():
+    a = BlockAllocator(5, 0, 16)
+    first = a.allocate_gpu_blocks(3)             # 0 1 2 ; free list: 3 4
+    a.free_gpu(first[1])                         # free list: 3 4 1
+    a.free_gpu(first[0])                         # free list: 3 4 1 0
+    assert a.allocate_gpu_blocks(4) == [3, 4, 1, 0]
 
 
-class TestSwap:
-    def test_swap_out_frees_gpu_allocates_cpu(self, allocator):
-        gpu_blocks = allocator.allocate_gpu_blocks(3)
-        mapping = allocator.swap_out(gpu_blocks)
-        assert allocator.num_free_gpu_blocks == 8
-        assert allocator.num_free_cpu_blocks == 1
-        assert set(mapping.keys()) == set(gpu_blocks)
-        assert all(0 <= v < 4 for v in mapping.values())
-
-    def test_swap_in_frees_cpu_allocates_gpu(self, allocator):
-        out_map = allocator.swap_out(allocator.allocate_gpu_blocks(3))
-        allocator.swap_in(list(out_map.values()))
-        assert allocator.num_free_cpu_blocks == 4
-        assert allocator.num_free_gpu_blocks == 5
-
-    def test_round_trip_mapping(self, allocator):
-        out_map = allocator.swap_out(allocator.allocate_gpu_blocks(2))
-        cpu = list(out_map.values())
-        in_map = allocator.swap_in(cpu)
-        new_gpu = [in_map[c] for c in cpu]
-        assert len(new_gpu) == 2 and all(0 <= g < 8 for g in new_gpu)
-
-
-class TestRefCount:
-    def test_ref_count_increments(self, allocator):
-        bid = allocator.allocate_gpu()
-        assert allocator.get_block(bid, "gpu").ref_count == 1
-
-    def test_partial_free(self, allocator):
-        bid = allocator.allocate_gpu()
-        block = allocator.get_block(bid)
-        block.ref_count += 1
-        allocator.free_gpu(bid)
-        assert block.ref_count == 1 and allocator.num_free_gpu_blocks == 7
-        allocator.free_gpu(bid)
-        assert allocator.num_free_gpu_blocks == 8
+def test_churn_matches_a_model_deque():
+    """Random alloc/free against a plain FIFO model of the same operations."""
+    rng = random.Random(11)
+    n = 40
+    a = BlockAllocator(n, 0, 16)
+    free = list(range(n))
+    held = []
+    for _ in range(2000):
+        if held and (rng.random() < 0.45 or not free):
+            bid = held.pop(rng.randrange(len(held)))
+            a.free_gpu(bid)
+            free.append(bid)
+        else:
+            k = rng.randint(1, 4)
+            if len(free) < k:
+                with pytest.raises(MemoryError):
+                    a.allocate_gpu_blocks(k)
+                continue
+            got = a.allocate_gpu_blocks(k)
+            assert got == free[:k]
+            del free[:k]
+            held += got
+        assert a.num_free_gpu_blocks == len(free)
 
 
-def test_fifo_order():
-    # block_allocator.py:40 popleft / :56 append: a freed id goes to the back.
-    a = BlockAllocator(4, 0, 16)
-    assert a.allocate_gpu_blocks(2) == [0, 1]
-    a.free_gpu(0)
-    assert a.allocate_gpu_blocks(3) == [2, 3, 0]
+def test_ref_counts():
+    a = BlockAllocator(3, 0, 16)
+    bid = a.allocate_gpu()
+    assert a.get_block(bid).ref_count == 1
+    a.get_block(bid).ref_count += 1              # a second holder
+    a.free_gpu(bid)
+    assert a.num_free_gpu_blocks == 2            # still held once
+    a.free_gpu(bid)
+    assert a.num_free_gpu_blocks == 3 and a.get_block(bid).ref_count == 0
 
 
-def test_fragmented_tables_are_disjoint_and_scattered():
-    blocks = [40, 7, 130, 1, 64]
-    tables = wl.tables_by_allocator(blocks, num_blocks=600, seed=5, cycles=2000)
-    flat = [b for t in tables for b in t]
+def test_exhaustion_raises_and_takes_nothing():
+    a = BlockAllocator(4, 2, 16)
+    a.allocate_gpu_blocks(3)
+    with pytest.raises(MemoryError):
+        a.allocate_gpu_blocks(2)
+    assert a.num_free_gpu_blocks == 1            # the failed request took no block
+    a.allocate_gpu()
+    with pytest.raises(MemoryError):
+        a.allocate_gpu()
+    a.allocate_cpu()
+    a.allocate_cpu()
+    with pytest.raises(MemoryError):
+        a.allocate_cpu()
+
+
+@pytest.mark.parametrize("pool", ["gpu", "cpu"])
+def test_double_free_is_an_assertion(pool):
+    a = BlockAllocator(2, 2, 16)
+    alloc, free = ((a.allocate_gpu, a.free_gpu) if pool == "gpu"
+                   else (a.allocate_cpu, a.free_cpu))
+    bid = alloc()
+    free(bid)
+    with pytest.raises(AssertionError):
+        free(bid)
+
+
+def test_swap_round_trip_maps_and_counts():
+    a = BlockAllocator(6, 4, 16)
+    gpu = a.allocate_gpu_blocks(3)
+    out = a.swap_out(gpu)
+    assert list(out) == gpu and sorted(out.values()) == [0, 1, 2]
+    assert a.num_free_gpu_blocks == 6 and a.num_free_cpu_blocks == 1
+    back = a.swap_in([out[g] for g in gpu])
+    assert list(back) == [out[g] for g in gpu]
+    assert a.num_free_cpu_blocks == 4 and a.num_free_gpu_blocks == 3
+    # the GPU ids come back from the FIFO list: the never-used 3, 4, 5 first
+    assert list(back.values()) == [3, 4, 5]
+
+
+def test_swap_out_beyond_the_cpu_pool_raises():
+    a = BlockAllocator(6, 2, 16)
+    with pytest.raises(MemoryError):
+        a.swap_out(a.allocate_gpu_blocks(3))
+
+
+def test_allocator_tables_are_disjoint_and_scattered():
+    blocks = [5, 40, 1, 17, 64]
+    tables = wl.tables_by_allocator(blocks, num_blocks=400, seed=3, cycles=500)
     assert [len(t) for t in tables] == blocks
-    assert len(set(flat)) == len(flat)
-    assert all(0 <= b < 600 for b in flat)
-    # scattered: most consecutive logical blocks are not physically adjacent
-    steps = sum(1 for t in tables for x, y in zip(t, t[1:]) if y != x + 1)
-    assert steps > 0.5 * sum(len(t) - 1 for t in tables)
-    again = wl.tables_by_allocator(blocks, num_blocks=600, seed=5, cycles=2000)
-    assert again == tables
+    flat = [b for t in tables for b in t]
+    assert len(set(flat)) == len(flat) and all(0 <= b < 400 for b in flat)
+    # churn leaves the free list out of order: some sequence holds non-consecutive ids
+    assert any(t != list(range(t[0], t[0] + len(t))) for t in tables if len(t) > 1)
+    assert tables == wl.tables_by_allocator(blocks, num_blocks=400, seed=3, cycles=500)

@@ -1,12 +1,21 @@
 """Continuous batching through the HIP path against the reference torch path (oracle).
 
-A small random-init Qwen2 (2 layers, 4/2 heads, head_dim 64) runs scheduler-driven
-steps: prompts of different lengths, mixed prefill + decode batches, block-table
-growth.  The GPU model (HIP kernels) and a CPU copy of the same weights whose
-attention seams are the oracle (attention.py:_prefill/_decode restated) see the
-same metadata every step; tokens are teacher-forced from the GPU side.  Logits
-must agree to |gpu - ref| <= 2e-2 + 1e-2 |ref|.  Greedy ties on random weights can
-flip, so the token streams themselves are not compared here.
+The GPU model (HIP kernels behind the Attention seams) and a CPU copy of the same weights
+whose attention seams are the oracle (attention.py:_prefill / _decode restated, RoPE as the
+reference's torch ops) see the same scheduler-built metadata every step; tokens are
+teacher-forced from the GPU side.  Logits of the toy model must agree to
+|gpu - ref| <= 2e-2 + 1e-2 |ref|.
+On random-init weights the logits are nearly flat, so greedy ties can flip between the two
+paths; the rate at which the two greedy picks agree is asserted against a floor only.
+
+  * a 2-layer toy Qwen2 (mixed prefill + decode batches, block-table growth);
+  * the real Qwen2-0.5B configuration of the end-to-end benchmark (24 layers, hidden 896,
+    14/2 heads, head_dim 64, FFN 4864, vocab 151936, bf16 weights ~N(0, 0.02)) on 8 of the
+    benchmark's requests (prompts U[64,1024]), with the benchmark's scheduler limits: every
+    attention call of every layer against the oracle on the same inputs (the tolerance
+    above, pool bytes exact), and the model's logits against the CPU model within bounds
+    set from the oracle's own bf16/fp32 spread (24 layers of bf16 GEMMs and attention);
+  * the engine running requests to completion.
 """
 import types
 
@@ -15,17 +24,19 @@ import pytest
 import torch
 
 from oracle import paged_ref
+from needle_amd import e2e
 from needle_amd.backend.block_allocator import BlockAllocator
 from needle_amd.backend.engine import LLMEngine
+from needle_amd.backend.request import SamplingParams, SeqState
 from needle_amd.backend.scheduler import Scheduler
-from needle_amd.backend.sequence import Request, SamplingParams, Sequence
-from needle_amd.model.config import ModelConfig
+from needle_amd.model.config import QWEN2_0_5B, ModelConfig
 from needle_amd.model.runner import ModelRunner
 from needle_amd.model.qwen2 import build_model, random_init_
 
 pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
 
-CFG = dict(model_type="qwen2", hidden_size=256, num_hidden_layers=2, num_attention_heads=4,
+TOY = dict(model_type="qwen2", hidden_size=256, num_hidden_layers=2, num_attention_heads=4,
            num_key_value_heads=2, intermediate_size=512, vocab_size=1000,
            max_position_embeddings=2048, rms_norm_eps=1e-6, rope_theta=1e6)
 
@@ -49,65 +60,211 @@ def oracle_runner(cfg, model_cpu):
     return r
 
 
-def _close(got, want):
+def _excess(got, want):
     got = got.float().cpu().numpy().astype(np.float64)
     want = want.float().numpy().astype(np.float64)
-    excess = np.abs(got - want) - (2e-2 + 1e-2 * np.abs(want))
-    assert np.isfinite(got).all() and excess.max() <= 0, float(np.abs(got - want).max())
+    assert np.isfinite(got).all()
+    return (np.abs(got - want) - (2e-2 + 1e-2 * np.abs(want))).max(), np.abs(got - want).max()
+
+
+def drive(cfg, gpu, cpu, sched, max_steps=60):
+    """Teacher-forced steps; returns (greedy agreements, picks, worst |diff|, steps, mixed)."""
+    agree = total = steps = mixed = 0
+    worst = 0.0
+    while sched.pending() and steps < max_steps:
+        plan = sched.schedule()
+        mixed += bool(plan.prefill and plan.decode)
+        picks, refs = [], []
+        for group, prefill in ((plan.prefill, True), (plan.decode, False)):
+            if not group:
+                continue
+            lg = gpu.forward(gpu.prepare_inputs(group, prefill))
+            lc = cpu.forward(cpu.prepare_inputs(group, prefill))
+            torch.cuda.synchronize()
+            excess, diff = _excess(lg, lc)
+            worst = max(worst, diff)
+            assert excess <= 0, f"step {steps}: logits differ by {diff:.4g}"
+            picks += lg.argmax(-1).tolist()
+            refs += lc.float().argmax(-1).tolist()
+        for s in plan.prefill:
+            s.kv_ready = True
+        agree += sum(a == b for a, b in zip(picks, refs))
+        total += len(picks)
+        for s, t in zip(plan.seqs, picks):
+            if s.push(t):
+                sched.finish(s)
+        steps += 1
+    assert not sched.pending()
+    return agree, total, worst, steps, mixed
+
+
+def _twin_runners(cfg, seed, nb):
+    gpu = ModelRunner(cfg, device=DEV, model=random_init_(build_model(cfg), seed))
+    cpu = oracle_runner(cfg, random_init_(build_model(cfg), seed))
+    gpu.init_kv_cache(nb)
+    cpu.init_kv_cache(nb)
+    return gpu, cpu
 
 
 @torch.no_grad()
-def test_continuous_batching_logits_match_reference_path():
-    cfg = ModelConfig(**CFG)
-    model = random_init_(build_model(cfg), seed=3)
-    gpu = ModelRunner(cfg, device="cuda:0", model=build_model(cfg))
-    gpu.model.load_state_dict(model.state_dict())
-    gpu.model.to(torch.bfloat16)
-    cpu = oracle_runner(cfg, model)
-    nb = 64
-    gpu.init_kv_cache(nb)
-    cpu.init_kv_cache(nb)
-    sched = Scheduler(BlockAllocator(nb, 0, 16), max_num_seqs=8, max_num_batched_tokens=600)
+def test_toy_model_logits_match_reference_path():
+    cfg = ModelConfig(**TOY)
+    gpu, cpu = _twin_runners(cfg, 3, 64)
+    sched = Scheduler(BlockAllocator(64, 0, 16), max_num_seqs=8, max_num_batched_tokens=600)
     rng = np.random.default_rng(0)
-    lens = [5, 31, 16, 70, 1, 120]
-    for i, n in enumerate(lens):
-        req = Request(f"r{i}", rng.integers(0, cfg.vocab_size, n).tolist(),
-                      SamplingParams(temperature=0.0, max_new_tokens=6 + i))
-        sched.add_sequence(Sequence(i + 1, req, list(req.prompt_token_ids),
-                                    list(range((n + 15) // 16)), 16))
-    steps = agree = total = 0
-    while sched.has_unfinished_seqs() and steps < 40:
-        out = sched.schedule()
-        seqs, logits = [], []
-        for group in (out.prefill_seqs, out.decode_seqs):
+    for i, n in enumerate([5, 31, 16, 70, 1, 120]):
+        sched.add(SeqState(i + 1, f"r{i}", rng.integers(0, cfg.vocab_size, n).tolist(),
+                           SamplingParams(temperature=0.0, max_new_tokens=6 + i)))
+    agree, total, worst, steps, mixed = drive(cfg, gpu, cpu, sched)
+    print(f"toy: greedy agreement {agree}/{total}, worst |diff| {worst:.3g}, {steps} steps")
+    assert agree >= 0.9 * total
+
+
+class SeamCheck:
+    """Checks every attention call of a GPU model against the oracle on the same inputs.
+
+    Each layer's forward is wrapped: its q/k/v projections are recomputed on the GPU (the
+    same GEMMs), the pool is copied before the call, and after it the oracle runs on the
+    host from those q/k/v, cos/sin, metadata and pool: RoPE as the reference's torch ops,
+    then write_kv + per-sequence SDPA (prefill) or the decode append + _decode_pytorch.
+    The layer's attention output (before o_proj) must be within the attention tolerance and
+    the pool after the call byte-equal to the oracle's."""
+
+    def __init__(self, model):
+        self.calls = 0
+        self.worst = 0.0
+        for layer in model.model.layers:
+            self._wrap(layer.self_attn)
+
+    def _wrap(self, att):
+        orig_forward = att.forward
+        check = self
+
+        def forward(hidden_states, positions, kv_cache, block_table, cu_seqlens, context_lens,
+                    max_seqlen, is_prefill, cos, sin):
+            t = hidden_states.shape[0]
+            q = att.q_proj(hidden_states).view(t, att.num_heads, att.head_dim).cpu()
+            k = att.k_proj(hidden_states).view(t, att.num_kv_heads, att.head_dim).cpu()
+            v = att.v_proj(hidden_states).view(t, att.num_kv_heads, att.head_dim).cpu()
+            pool = kv_cache.cpu()
+            seen = {}
+            attend = att._prefill_attend if is_prefill else att._decode_attend
+
+            def capture(*a, **kw):
+                seen["out"] = attend(*a, **kw)
+                return seen["out"]
+            name = "_prefill_attend" if is_prefill else "_decode_attend"
+            setattr(att, name, capture)
+            try:
+                y = orig_forward(hidden_states, positions, kv_cache, block_table, cu_seqlens,
+                                 context_lens, max_seqlen, is_prefill, cos, sin)
+            finally:
+                delattr(att, name)
+            qr, kr = paged_ref.apply_rope(q, k, cos.cpu(), sin.cpu())
+            if is_prefill:
+                want = paged_ref.prefill(qr, kr, v, pool, block_table.cpu(), cu_seqlens.cpu(),
+                                         context_lens.cpu(), att.num_heads, att.num_kv_heads)
+            else:
+                want = paged_ref.decode(qr, kr, v, pool, block_table.cpu(), context_lens.cpu(),
+                                        att.scale, att.num_heads, att.num_kv_heads,
+                                        att.head_dim)
+            excess, diff = _excess(seen["out"], want)
+            check.worst = max(check.worst, diff)
+            assert excess <= 0, f"layer {att.layer_idx}: attention differs by {diff:.4g}"
+            assert torch.equal(kv_cache.cpu().view(torch.int16), pool.view(torch.int16)), \
+                f"layer {att.layer_idx}: pool bytes differ from the oracle's"
+            check.calls += 1
+            return y
+        att.forward = forward
+
+
+def _qwen_requests(sched):
+    for i, (rid, prompt, _olen) in enumerate(e2e.requests(8)):
+        # the first two finish early, so the two that wait are admitted next to decoders
+        sched.add(SeqState(i + 1, rid, prompt,
+                           SamplingParams(temperature=0.0, max_new_tokens=3 if i < 2 else 7)))
+
+
+@torch.no_grad()
+def test_qwen2_05b_every_attention_call_matches_the_oracle():
+    """The real Qwen2-0.5B configuration, 8 benchmark requests through the scheduler: all
+    24 layers' attention calls of every prefill and decode forward against the oracle."""
+    cfg = ModelConfig(**QWEN2_0_5B)
+    nb = 800
+    gpu = ModelRunner(cfg, device=DEV, model=random_init_(build_model(cfg), e2e.E2E_SEED))
+    gpu.init_kv_cache(nb)
+    check = SeamCheck(gpu.model)
+    sched = Scheduler(BlockAllocator(nb, 0, 16), max_num_seqs=6, max_num_batched_tokens=8192)
+    _qwen_requests(sched)
+    steps = mixed = 0
+    while sched.pending():
+        plan = sched.schedule()
+        mixed += bool(plan.prefill and plan.decode)
+        toks = []
+        for group, pre in ((plan.prefill, True), (plan.decode, False)):
+            if group:
+                toks += gpu.forward(gpu.prepare_inputs(group, pre)).argmax(-1).tolist()
+        for s in plan.prefill:
+            s.kv_ready = True
+        for s, t in zip(plan.seqs, toks):
+            if s.push(t):
+                sched.finish(s)
+        steps += 1
+    print(f"qwen2-0.5b seams: {check.calls} attention calls, worst |diff| {check.worst:.3g}, "
+          f"{steps} steps, {mixed} mixed", flush=True)
+    assert mixed >= 1 and check.calls == 24 * (steps + mixed)
+
+
+# Full-model logits after 24 bf16 layers carry the GEMM and attention rounding of every
+# layer.  Measured on the oracle itself: computing only its attention in fp32 instead of
+# bf16 moves these prefill logits (std 0.60) by up to 0.0625, relative L2 2.0%.  The GPU
+# path is held to about twice that.
+LOGITS_MAX_DIFF = 0.15
+LOGITS_REL_L2 = 0.04
+
+
+@torch.no_grad()
+def test_qwen2_05b_teacher_forced_logits():
+    cfg = ModelConfig(**QWEN2_0_5B)
+    nb = 800
+    gpu, cpu = _twin_runners(cfg, e2e.E2E_SEED, nb)
+    sched = Scheduler(BlockAllocator(nb, 0, 16), max_num_seqs=6, max_num_batched_tokens=8192)
+    _qwen_requests(sched)
+    agree = total = steps = 0
+    worst, worst_rel = 0.0, 0.0
+    while sched.pending():
+        plan = sched.schedule()
+        picks, refs = [], []
+        for group, pre in ((plan.prefill, True), (plan.decode, False)):
             if not group:
                 continue
-            pre = not group[0].prefilled
-            lg = gpu.forward(gpu.prepare_inputs(group, out.block_tables, pre))
-            lc = cpu.forward(cpu.prepare_inputs(group, out.block_tables, pre))
-            torch.cuda.synchronize()
-            _close(lg, lc)
-            seqs += group
-            logits.append((lg.float().cpu(), lc.float()))
-        for s in out.prefill_seqs:
-            s.prefilled = True
-        toks = torch.cat([g for g, _ in logits]).argmax(-1).tolist()
-        ref = torch.cat([c for _, c in logits]).argmax(-1).tolist()
-        agree += sum(a == b for a, b in zip(toks, ref))
-        total += len(toks)
-        for s, t in zip(seqs, toks):
-            s.append_token(t)
-            if s.num_generated_tokens >= s.request.sampling_params.max_new_tokens:
-                sched.free_sequence(s)
+            lg = gpu.forward(gpu.prepare_inputs(group, pre)).float().cpu()
+            lc = cpu.forward(cpu.prepare_inputs(group, pre)).float()
+            assert torch.isfinite(lg).all()
+            d = (lg - lc).abs()
+            worst = max(worst, float(d.max()))
+            worst_rel = max(worst_rel, float(d.norm() / lc.norm()))
+            picks += lg.argmax(-1).tolist()
+            refs += lc.argmax(-1).tolist()
+        for s in plan.prefill:
+            s.kv_ready = True
+        agree += sum(a == b for a, b in zip(picks, refs))
+        total += len(picks)
+        for s, t in zip(plan.seqs, picks):
+            if s.push(t):
+                sched.finish(s)
         steps += 1
-    assert not sched.has_unfinished_seqs()
-    print(f"greedy agreement {agree}/{total}")
+    print(f"qwen2-0.5b logits: max |diff| {worst:.4g}, relative L2 {worst_rel:.4g}, "
+          f"greedy agreement {agree}/{total}", flush=True)
+    assert worst <= LOGITS_MAX_DIFF and worst_rel <= LOGITS_REL_L2
+    assert agree >= 0.8 * total
 
 
 @torch.no_grad()
 def test_engine_runs_requests_to_completion():
-    cfg = ModelConfig(**CFG)
-    eng = LLMEngine(cfg, max_gpu_blocks=256, seed=1)
+    cfg = ModelConfig(**TOY)
+    eng = LLMEngine(cfg, max_gpu_blocks=256, seed=1, decode_graphs=True, max_model_len=512,
+                    max_num_seqs=16)
     rng = np.random.default_rng(1)
     want = {}
     for i in range(12):
@@ -119,7 +276,7 @@ def test_engine_runs_requests_to_completion():
     while eng.has_unfinished_requests():
         got.update(eng.step())
     assert {k: len(v) for k, v in got.items()} == want
-    assert eng.allocator.num_free_gpu_blocks == 256
+    assert eng.allocator.num_free_gpu_blocks == 255          # one block is the graphs' scratch
     assert all(0 <= t < cfg.vocab_size for v in got.values() for t in v)
     # the same greedy request twice gives the same tokens (the cache is reused correctly)
     a = eng.generate([5, 6, 7] * 20, SamplingParams(temperature=0.0, max_new_tokens=8), "a")
