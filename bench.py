@@ -13,14 +13,16 @@ Printed (one JSON line):
   value         algorithmic bytes of the whole step / step time   (GB/s); the step is
                 captured once as a HIP graph and replayed, as a serving loop replays its
                 decode steps (ms_per_step_eager: the same step launched from Python)
-  roofline      paged decode alone (attention + partition merge): algorithmic bytes per
-                launch / average launch time over graph replays of the 32 layers, timed
-                with events on the launch stream, vs the 8 TB/s HBM peak
+  roofline      the step's launch pair per layer (fused append + paged decode, merge):
+                algorithmic bytes per pair / average pair time over graph replays of the
+                32 layers, timed with events on the launch stream, vs the 8 TB/s HBM peak;
+                traffic from the committed counter summary of the same pair
   cpu_baseline  the CPU restatement of the reference torch path, one layer
                 of the same workload, on this host's cores
-  other_shapes  Qwen2-0.5B layer decode, Qwen2-7B varlen prefill, Llama-3-8B long-context
-                decode, and end-to-end continuous batching on random-init Qwen2-0.5B
-                (output tokens/s, the reference benchmark's definition)
+  other_shapes  Qwen2-0.5B layer decode (cache-resident, and cold over 128 pools),
+                Qwen2-7B varlen append + prefill, Llama-3-8B long-context decode, and
+                end-to-end continuous batching on random-init Qwen2-0.5B (output tokens/s,
+                the reference benchmark's definition), each with its CPU baseline
 Algorithmic bytes: every attended K/V row once, q in, output out, the block
 table entries and context lengths read; for append, k/v rows read and
 written plus their slot indices.
@@ -87,20 +89,68 @@ def build_workload(torch, wl, device):
     return shape, ctx, tables, num_blocks, bt, ctx_t, pools, qs, ks, vs, outs
 
 
-TRAFFIC_PROFILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                               "paged_decode_llama3_8b_hbm_traffic.md")
+ROOT = os.path.dirname(os.path.abspath(__file__))
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "paged_decode_llama3_8b_hbm_traffic.md")
+DECODE_SOURCE = os.path.join(ROOT, "needle_amd", "csrc", "paged_decode.hip")
+
+
+def source_sha16(path=DECODE_SOURCE):
+    import hashlib
+    with open(path, "rb") as f:
+        return hashlib.sha256(f.read()).hexdigest()[:16]
 
 
 def measured_traffic():
-    """HBM bytes per decode launch from the committed FETCH_SIZE/WRITE_SIZE summary (or None)."""
+    """HBM bytes per timed decode launch pair from the committed FETCH_SIZE/WRITE_SIZE summary.
+
+    The summary names the kernels it counted and the hash of the decode source it was
+    counted on; when that source has changed since, the figure no longer describes the
+    timed kernels and is not reported (None, with the reason)."""
+    info = {}
     try:
         with open(TRAFFIC_PROFILE) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch:"):
-                    return int(line.split(":")[1])
+                if ":" in line and line.split(":")[0] in (
+                        "traffic_bytes_per_launch", "kernel_source_sha16", "kernels"):
+                    key, val = line.split(":", 1)
+                    info[key] = val.strip()
+    except OSError:
+        return None, "no traffic summary committed"
+    if "traffic_bytes_per_launch" not in info:
+        return None, "traffic summary has no traffic_bytes_per_launch line"
+    now = source_sha16()
+    if info.get("kernel_source_sha16") != now:
+        print(f"bench.py: {TRAFFIC_PROFILE} was counted on paged_decode.hip "
+              f"{info.get('kernel_source_sha16')}, the source is now {now}: traffic not "
+              "reported", file=sys.stderr, flush=True)
+        return None, (f"stale: counted on paged_decode.hip {info.get('kernel_source_sha16')}, "
+                      f"source now {now}")
+    return int(info["traffic_bytes_per_launch"]), info.get("kernels", "")
+
+
+def host_info(torch):
+    threads = len(os.sched_getaffinity(0))
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
     except OSError:
         pass
-    return None
+    return {"cores": threads, "cpu_model": model, "torch": torch.__version__}
+
+
+def cpu_timed(fn, budget_s, max_reps=1000, min_reps=1):
+    """(reps, seconds): fn() repeated until budget_s has passed (at least min_reps times)."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if (el >= budget_s and reps >= min_reps) or reps >= max_reps:
+            return reps, el
 
 
 def time_region(torch, fn, reps):
@@ -162,51 +212,163 @@ def e2e_measurement(torch, time_limit_s):
                         "256 seqs / 8192 tokens, decode steps replayed from HIP graphs"}
 
 
-def extra_measurements(torch, ops, wl, reps):
-    """The other four shapes, one launch sequence each (event timing on the launch stream)."""
-    dev = torch.device("cuda:0")
-    res = {}
+def e2e_cpu_subset(torch, n_requests=8, max_new=32):
+    """The end-to-end subset on both paths: the GPU engine runs the first n_requests of the
+    benchmark (outputs capped at max_new), then a CPU runner with the same weights whose
+    attention seams are the oracle (the reference torch path) replays the same schedule
+    teacher-forced with the GPU's tokens.  Reports the CPU path's output tok/s on that
+    subset and how often its greedy pick agrees with the GPU's."""
+    import copy
+    import types
+    from needle_amd import e2e
+    from needle_amd.backend.block_allocator import BlockAllocator
+    from needle_amd.backend.request import SamplingParams, SeqState
+    from needle_amd.backend.scheduler import Scheduler
+    from needle_amd.model.config import QWEN2_0_5B, ModelConfig
+    from needle_amd.model.qwen2 import build_model, random_init_
+    from needle_amd.model.runner import ModelRunner
+    from oracle import paged_ref
 
-    # Qwen2-0.5B layer decode, 8 sequences: ~1 MB working set, cache-resident.
+    cfg = ModelConfig(**QWEN2_0_5B)
+    base = random_init_(build_model(cfg), e2e.E2E_SEED)
+    reqs = [(rid, p, min(o, max_new)) for rid, p, o in e2e.requests(n_requests)]
+    nb = 2048
+    gpu = ModelRunner(cfg, device="cuda:0", model=copy.deepcopy(base))
+    cpu = ModelRunner(cfg, device="cpu", model=base)
+    for layer in cpu.model.model.layers:
+        att = layer.self_attn
+        att.fuse_rope = False
+        att._prefill = types.MethodType(
+            lambda self, q, k, v, kv, bt, cu, ctx, ms: paged_ref.prefill(
+                q, k, v, kv, bt, cu, ctx, self.num_heads, self.num_kv_heads), att)
+        att._decode = types.MethodType(
+            lambda self, q, k, v, kv, bt, ctx: paged_ref.decode(
+                q, k, v, kv, bt, ctx, self.scale, self.num_heads, self.num_kv_heads,
+                self.head_dim), att)
+    results = {}
+    schedule = []                   # per step: [(group, is_prefill, gpu tokens)]
+    for side, runner in (("gpu", gpu), ("cpu", cpu)):
+        runner.init_kv_cache(nb)
+        sched = Scheduler(BlockAllocator(nb, 0, 16), 256, 8192)
+        for i, (rid, prompt, olen) in enumerate(reqs):
+            sched.add(SeqState(i + 1, rid, prompt, SamplingParams(temperature=0.0,
+                                                                  max_new_tokens=olen)))
+        n_tok, agree, step = 0, 0, 0
+        if side == "gpu":
+            torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        while sched.pending():
+            plan = sched.schedule()
+            toks = []
+            for group, pre in ((plan.prefill, True), (plan.decode, False)):
+                if group:
+                    lg = runner.forward(runner.prepare_inputs(group, pre))
+                    toks += lg.argmax(-1).tolist()
+            for s in plan.prefill:
+                s.kv_ready = True
+            if side == "gpu":
+                schedule.append(toks)
+                forced = toks
+            else:
+                forced = schedule[step]
+                agree += sum(a == b for a, b in zip(toks, forced))
+            for s, t in zip(plan.seqs, forced):
+                n_tok += 1
+                if s.push(t):
+                    sched.finish(s)
+            step += 1
+        el = time.perf_counter() - t0
+        results[side] = (n_tok, el, agree)
+    del gpu
+    torch.cuda.empty_cache()
+    n_tok, el, agree = results["cpu"]
+    return {"value": round(n_tok / el, 2), "unit": "output tok/s",
+            "kind": "port", **host_info(torch),
+            "sample": f"the first {n_requests} benchmark requests, outputs capped at {max_new} "
+                      f"tokens ({n_tok} tokens, {el:.1f} s), eager CPU runner with the oracle "
+                      "attention seams, teacher-forced with the GPU engine's tokens",
+            "gpu_eager_tok_per_s_same_subset": round(results["gpu"][0] / results["gpu"][1], 1),
+            "greedy_agreement": round(agree / max(1, n_tok), 4)}
+
+
+def qwen05b_decode(torch, ops, wl, reps, cpu_budget, cold_pools=1024, cpu=True):
+    """Qwen2-0.5B layer decode (8 sequences, ~1.1 MB attended): cache-resident latency from a
+    graph of 24 fused launches, a cold variant over cold_pools distinct 4 MiB pools (4 GiB in
+    all; the attended bytes of one replay, ~1.1 GB, are four times the 256 MiB Infinity
+    Cache, so they stream from HBM), and the CPU path."""
+    from oracle import paged_ref
+    dev = torch.device("cuda:0")
     c1 = wl.config_case("qwen2-0.5b-decode", device=dev, garbage=False)
     s1 = c1.shape
 
-    def dec1():
+    def fused(pool, out=None):
         # the layer's _decode (attention.py:141-159): append + attention in one launch
-        ops.paged_decode(c1.q, c1.kv_cache, c1.block_table, c1.context_lens, s1.scale,
-                         s1.num_heads, s1.num_kv_heads, s1.head_dim, new_k=c1.k, new_v=c1.v)
+        return ops.paged_decode(c1.q, pool, c1.block_table, c1.context_lens, s1.scale,
+                                s1.num_heads, s1.num_kv_heads, s1.head_dim, new_k=c1.k,
+                                new_v=c1.v, out=out)
 
-    def dec1_separate():
-        ops.kv_append(c1.k, c1.v, c1.kv_cache, c1.block_table, c1.context_lens)
-        ops.paged_decode(c1.q, c1.kv_cache, c1.block_table, c1.context_lens, s1.scale,
+    def separate(pool):
+        ops.kv_append(c1.k, c1.v, pool, c1.block_table, c1.context_lens)
+        ops.paged_decode(c1.q, pool, c1.block_table, c1.context_lens, s1.scale,
                          s1.num_heads, s1.num_kv_heads, s1.head_dim)
-    dec1()
-    ms1_eager = time_region(torch, dec1, reps * 10)
-    layers1 = 24
+    fused(c1.kv_cache)
+    ms_eager = time_region(torch, lambda: fused(c1.kv_cache), reps * 10)
+    layers = 24
 
-    def per_layer_graph(fn):
-        def layers():
-            for _ in range(layers1):
-                fn()
-        g = capture(torch, layers)
-        ms = time_region(torch, g.replay, reps) / layers1
+    def per_launch_graph(fns):
+        def run():
+            for f in fns:
+                f()
+        g = capture(torch, run)
+        ms = time_region(torch, g.replay, reps) / len(fns)
         del g
         return ms
-    ms1 = per_layer_graph(dec1)
-    ms1_sep = per_layer_graph(dec1_separate)
-    b1 = wl.decode_bytes(s1, c1.ctx, c1.block_table.shape[1]) + \
+    ms = per_launch_graph([lambda: fused(c1.kv_cache)] * layers)
+    ms_sep = per_launch_graph([lambda: separate(c1.kv_cache)] * layers)
+    nbytes = wl.decode_bytes(s1, c1.ctx, c1.block_table.shape[1]) + \
         wl.append_bytes(s1, c1.num_seqs, c1.num_seqs, varlen=False)
-    res["qwen2_0.5b_decode"] = {"us_per_layer": round(ms1 * 1e3, 2),
-                                "us_per_layer_eager": round(ms1_eager * 1e3, 2),
-                                "us_per_layer_separate_launches": round(ms1_sep * 1e3, 2),
-                                "effective_gbs": round(b1 / ms1 / 1e6, 1),
-                                "note": "append + decode of 8 sequences (one fused launch per "
-                                        "layer), 24 layers replayed from one HIP graph; ~1 MB "
-                                        "working set stays in L2/MALL (cache-resident, not an "
-                                        "HBM figure)"}
+    # cold: every launch of the graph reads a different 4 MiB pool
+    gen = torch.Generator(device=dev).manual_seed(11)
+    pools = [torch.randn(c1.kv_cache.shape, generator=gen, device=dev, dtype=torch.float32)
+             .to(torch.bfloat16) for _ in range(cold_pools)]
+    out = torch.empty_like(c1.q)
+    ms_cold = per_launch_graph([(lambda p=p: fused(p, out)) for p in pools])
+    pool_mib = c1.kv_cache.numel() * 2 / 2 ** 20
+    del pools
+    torch.cuda.empty_cache()
+    res = {}
+    if cpu:   # the CPU path: append + _decode_pytorch on the host, same inputs
+        cc = c1.to("cpu")
+        reps_c, el = cpu_timed(lambda: paged_ref.decode(
+            cc.q, cc.k, cc.v, cc.kv_cache, cc.block_table, cc.context_lens, s1.scale,
+            s1.num_heads, s1.num_kv_heads, s1.head_dim), cpu_budget, min_reps=3)
+        res["cpu_baseline"] = {"us_per_layer": round(el / reps_c * 1e6, 1),
+                               "gbs": round(nbytes * reps_c / el / 1e9, 3), "kind": "port",
+                               **host_info(torch),
+                               "sample": f"append + decode of the same 8 sequences, {reps_c} "
+                                         f"reps in {el:.1f} s"}
+        del cc
     del c1
+    return {"us_per_layer": round(ms * 1e3, 2),
+            "us_per_layer_eager": round(ms_eager * 1e3, 2),
+            "us_per_layer_separate_launches": round(ms_sep * 1e3, 2),
+            "effective_gbs_cache_resident": round(nbytes / ms / 1e6, 1),
+            "algorithmic_bytes": nbytes,
+            "cold": {"us_per_launch": round(ms_cold * 1e3, 2),
+                     "gbs": round(nbytes / ms_cold / 1e6, 1),
+                     "frac_of_hbm_peak": round(nbytes / ms_cold / 1e6 / HBM_PEAK_GBS, 4),
+                     "pools": cold_pools, "pool_mib": round(pool_mib, 2),
+                     "note": "one graph of fused launches, each over its own pool; the bytes "
+                             "one replay attends are ~4x the Infinity Cache: HBM-resident"},
+            **res,
+            "note": "append + decode of 8 sequences, one fused launch per layer; 24 launches "
+                    "replayed from one HIP graph on one ~1 MB working set (cache-resident)"}
 
-    # Qwen2-7B varlen prefill: append all prompt tokens, then causal attention.
+
+def qwen7b_prefill(torch, ops, wl, reps, cpu=True):
+    """Qwen2-7B varlen append + causal prefill (GPU) and the CPU path (one repetition)."""
+    from oracle import paged_ref
+    dev = torch.device("cuda:0")
     c3 = wl.config_case("qwen2-7b-prefill", device=dev, garbage=False)
     s3 = c3.shape
 
@@ -245,11 +407,11 @@ def extra_measurements(torch, ops, wl, reps):
     rb = 2 * t3 * s3.num_heads * s3.head_dim * 2 + 2 * t3 * s3.head_dim * 2 + ab
     app3()   # the cache holds k again (the rotated rows only changed its values)
     # The prefill is compute-bound: its clock ramps over ~1 s of load, so it is timed right
-    # after 1.5 s of warm-up launches.
+    # after 1.5 s of warm-up launches, over 50 launches.
     warm(torch, att3, 1.5)
-    ms_p = time_region(torch, att3, reps)
+    ms_p = time_region(torch, att3, 50)
     fl = wl.prefill_flops(s3, c3.new_lens)
-    res["qwen2_7b_prefill"] = {
+    res = {
         "tokens": t3, "append_us": round(ms_a * 1e3, 2),
         "append_gbs": round(ab / ms_a / 1e6, 1),
         "append_frac_of_hbm_peak": round(ab / ms_a / 1e6 / HBM_PEAK_GBS, 4),
@@ -259,28 +421,78 @@ def extra_measurements(torch, ops, wl, reps):
         "attention_us": round(ms_p * 1e3, 2),
         "attention_tflops": round(fl / ms_p / 1e9, 1),
         "attention_frac_of_mfma_peak": round(fl / ms_p / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "attention_launches_timed": 50,
         "algorithmic_flops": fl}
+    if cpu:
+        cc = c3.to("cpu")
+        t0 = time.perf_counter()
+        paged_ref.write_kv(cc.k, cc.v, cc.kv_cache, cc.block_table, cc.cu_seqlens,
+                           cc.context_lens)
+        t_app = time.perf_counter() - t0
+        paged_ref.prefill_pytorch(cc.q, cc.k, cc.v, cc.cu_seqlens, s3.num_heads,
+                                  s3.num_kv_heads)
+        t_att = time.perf_counter() - t0 - t_app
+        res["cpu_baseline"] = {"append_gbs": round(ab / t_app / 1e9, 3),
+                               "attention_tflops": round(fl / t_att / 1e12, 4),
+                               "ms": round((t_app + t_att) * 1e3, 1), "kind": "port",
+                               **host_info(torch),
+                               "sample": "one repetition of write_kv + per-prompt causal SDPA "
+                                         "(the reference torch path) on the same 16 prompts"}
+        del cc
     del c3
+    return res
 
-    # Llama-3-8B long-context fragmented decode, 256 sequences, allocator-churned tables.
+
+def long_context_decode(torch, ops, wl, reps, cpu=True):
+    """Llama-3-8B long-context fragmented decode, 256 sequences, allocator-churned tables."""
+    from oracle import paged_ref
+    dev = torch.device("cuda:0")
     c5 = wl.config_case("llama3-8b-long-decode", device=dev, garbage=False)
     s5 = c5.shape
 
     def dec5():
+        ops.paged_decode(c5.q, c5.kv_cache, c5.block_table, c5.context_lens, s5.scale,
+                         s5.num_heads, s5.num_kv_heads, s5.head_dim, new_k=c5.k, new_v=c5.v)
+
+    def dec5_separate():
         ops.kv_append(c5.k, c5.v, c5.kv_cache, c5.block_table, c5.context_lens)
         ops.paged_decode(c5.q, c5.kv_cache, c5.block_table, c5.context_lens, s5.scale,
                          s5.num_heads, s5.num_kv_heads, s5.head_dim)
     dec5()
-    ms5 = time_region(torch, dec5, max(3, reps // 4))
+    n = max(5, reps // 2)
+    ms5 = time_region(torch, dec5, n)
+    ms5_sep = time_region(torch, dec5_separate, n)
     b5 = wl.decode_bytes(s5, c5.ctx, c5.block_table.shape[1]) + \
         wl.append_bytes(s5, c5.num_seqs, c5.num_seqs, varlen=False)
-    res["llama3_8b_long_context_decode"] = {
-        "ms": round(ms5, 4), "gbs": round(b5 / ms5 / 1e6, 1),
-        "frac_of_hbm_peak": round(b5 / ms5 / 1e6 / HBM_PEAK_GBS, 4),
-        "context_tokens": sum(c5.ctx), "lognormal_sigma": wl.LONG_CONTEXT_SIGMA}
-    del c5
+    res = {"ms": round(ms5, 4), "gbs": round(b5 / ms5 / 1e6, 1),
+           "frac_of_hbm_peak": round(b5 / ms5 / 1e6 / HBM_PEAK_GBS, 4),
+           "ms_separate_launches": round(ms5_sep, 4),
+           "algorithmic_bytes": b5, "launches_timed": n,
+           "context_tokens": sum(c5.ctx), "lognormal_sigma": wl.LONG_CONTEXT_SIGMA}
+    if cpu:
+        cc = c5.to("cpu")
+        del c5
+        torch.cuda.empty_cache()
+        t0 = time.perf_counter()
+        paged_ref.decode(cc.q, cc.k, cc.v, cc.kv_cache, cc.block_table, cc.context_lens,
+                         s5.scale, s5.num_heads, s5.num_kv_heads, s5.head_dim)
+        el = time.perf_counter() - t0
+        res["cpu_baseline"] = {"gbs": round(b5 / el / 1e9, 3), "ms": round(el * 1e3, 1),
+                               "kind": "port", **host_info(torch),
+                               "sample": "one repetition of append + _decode_pytorch over all "
+                                         "256 sequences (the 12 GB pool copied to host memory)"}
+        del cc
+    else:
+        del c5
     torch.cuda.empty_cache()
     return res
+
+
+def extra_measurements(torch, ops, wl, reps, cpu_budget, cpu=True):
+    """The other shapes, each with its CPU baseline (the reference torch path restated)."""
+    return {"qwen2_0.5b_decode": qwen05b_decode(torch, ops, wl, reps, cpu_budget, cpu=cpu),
+            "qwen2_7b_prefill": qwen7b_prefill(torch, ops, wl, reps, cpu=cpu),
+            "llama3_8b_long_context_decode": long_context_decode(torch, ops, wl, reps, cpu=cpu)}
 
 
 def ceilings(torch):
@@ -346,25 +558,18 @@ def sdpa_ceiling(torch):
 def cpu_baseline(torch, wl, shape, ctx, budget_s):
     """The reference torch path on the CPU (append + _decode_pytorch), one layer, repeated."""
     from oracle import paged_ref
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
+    info = host_info(torch)
+    torch.set_num_threads(info["cores"])
     case = wl.decode_case(shape, ctx, seed=SEED, device="cpu", garbage=False)
     per_layer = wl.decode_bytes(shape, ctx, case.block_table.shape[1]) + \
         wl.append_bytes(shape, len(ctx), len(ctx), varlen=False)
-    reps, t0 = 0, time.perf_counter()
-    while True:
-        paged_ref.decode(case.q, case.k, case.v, case.kv_cache, case.block_table,
-                         case.context_lens, shape.scale, shape.num_heads, shape.num_kv_heads,
-                         shape.head_dim)
-        reps += 1
-        el = time.perf_counter() - t0
-        if el >= budget_s or reps >= 1000:
-            break
-    return {"value": round(per_layer * reps / el / 1e9, 3), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+    reps, el = cpu_timed(lambda: paged_ref.decode(
+        case.q, case.k, case.v, case.kv_cache, case.block_table, case.context_lens,
+        shape.scale, shape.num_heads, shape.num_kv_heads, shape.head_dim), budget_s)
+    return {"value": round(per_layer * reps / el / 1e9, 3), "unit": "GB/s", "kind": "port",
+            **info,
             "sample": f"one layer of the same workload (64 seqs, append + decode), "
-                      f"{reps} reps in {el:.1f} s, torch {torch.__version__} CPU, "
-                      f"{threads} threads"}
+                      f"{reps} reps in {el:.1f} s"}
 
 
 def main():
@@ -405,6 +610,21 @@ def main():
                          partition_tokens=args.partition, out=outs[l], workspace=ws,
                          new_k=ks[l], new_v=vs[l])
 
+    # The engine's decode step (Attention.forward from RoPE on): the rotary embedding of q
+    # and of the new key row folded into the same launch, cos/sin at each sequence's position.
+    from needle_amd.layers.rope import RotaryEmbedding
+    rope_tab = RotaryEmbedding(d, 8192, 5e5).to(device=dev, dtype=torch.bfloat16)
+    cos_t, sin_t = rope_tab.get_cos_sin(ctx_t.long())
+
+    def rope_layer(l):
+        ops.paged_decode(qs[l], pools[l], bt, ctx_t, sc, h, hkv, d,
+                         partition_tokens=args.partition, out=outs[l], workspace=ws,
+                         new_k=ks[l], new_v=vs[l], cos=cos_t, sin=sin_t)
+
+    def step_rope():
+        for l in range(LAYERS):
+            rope_layer(l)
+
     def step_separate():
         for l in range(LAYERS):
             append_layer(l)
@@ -417,10 +637,11 @@ def main():
     if args.profile:
         info = {"profile": args.profile, "profile_steps": args.steps}
         if args.profile == "decode":
-            for _ in range(args.steps):   # separate launches: the counters per kernel
-                step_separate()
-            info.update(layers=LAYERS,
-                        decode_algorithmic_bytes_per_launch=wl.decode_bytes(shape, ctx, width))
+            for _ in range(args.steps):   # the timed step: fused append + attention, merge
+                step()
+            info.update(layers=LAYERS, kernel_source_sha16=source_sha16(),
+                        algorithmic_bytes_per_launch_pair=wl.decode_bytes(shape, ctx, width)
+                        + wl.append_bytes(shape, len(ctx), len(ctx), varlen=False))
         else:
             del pools
             torch.cuda.empty_cache()
@@ -450,6 +671,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
+    warm(torch, step, 1.0)       # the clock settles before the first timed region
     ms_step_eager = time_region(torch, step, args.steps)
 
     # The same step captured once as a HIP graph and replayed, as a serving loop runs
@@ -459,6 +681,9 @@ def main():
     g_sep = capture(torch, step_separate)
     ms_step_separate = time_region(torch, g_sep.replay, args.steps)
     del g_sep
+    g_rope = capture(torch, step_rope)
+    ms_step_rope = time_region(torch, g_rope.replay, args.steps)
+    del g_rope
 
     # per-op timings over the same rotating pools, each a graph of its 32 launches
     def decode_all():
@@ -477,8 +702,10 @@ def main():
     dec_b = wl.decode_bytes(shape, ctx, width)
     app_b = wl.append_bytes(shape, len(ctx), len(ctx), varlen=False)
     value = LAYERS * (dec_b + app_b) / (ms_step / 1e3) / 1e9
+    pair_us = ms_step * 1e3 / LAYERS          # one fused launch + merge per layer
     dec_gbs = dec_b / (ms_dec / 1e3) / 1e9
     app_gbs = app_b / (ms_app / 1e3) / 1e9
+    traffic, traffic_kernels = measured_traffic()
 
     result = {
         "metric": "paged decode attn HBM GB/s (% of peak); KV-append GB/s; e2e output tok/s",
@@ -490,6 +717,7 @@ def main():
         "ms_per_step": round(ms_step, 4),
         "ms_per_step_eager": round(ms_step_eager, 4),
         "ms_per_step_separate_launches": round(ms_step_separate, 4),
+        "ms_per_step_with_rope": round(ms_step_rope, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -505,27 +733,40 @@ def main():
             "decode_split": "per-sequence workgroups" if ws_bytes <= 256 else "stream split",
         },
         "roofline": {
-            "bound": "hbm", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
-            "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(),
+            "bound": "hbm", "achieved": round(value, 1), "peak": HBM_PEAK_GBS,
+            "unit": "GB/s", "frac": round(value / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "traffic_kernels": traffic_kernels,
             "traffic_source": "profiles/paged_decode_llama3_8b_hbm_traffic.md (rocprofv3 "
-                              "FETCH_SIZE x2 + WRITE_SIZE x1, scaled by a 1 GiB copy)",
-            "kernel": "paged decode (attention + partition merge), per layer launch",
-            "algorithmic_bytes_per_launch": dec_b, "avg_launch_us": round(ms_dec * 1e3, 2),
+                              "FETCH_SIZE x2 + WRITE_SIZE x1 per launch pair, scaled by a "
+                              "1 GiB copy; keyed to the hash of paged_decode.hip)",
+            "kernel": "the timed step's launch pair per layer: fused append + paged decode "
+                      "attention (ndl_paged_decode_append) and the partition merge",
+            "algorithmic_bytes_per_launch": dec_b + app_b, "avg_launch_us": round(pair_us, 2),
         },
+        "decode_only": {"achieved_gbs": round(dec_gbs, 1),
+                        "frac_of_hbm_peak": round(dec_gbs / HBM_PEAK_GBS, 4),
+                        "avg_launch_us": round(ms_dec * 1e3, 2),
+                        "algorithmic_bytes_per_launch": dec_b,
+                        "note": "ndl_paged_decode (attention + merge, no append) over the same "
+                                "32 pools"},
         "kv_append": {"achieved_gbs": round(app_gbs, 1), "avg_launch_us": round(ms_app * 1e3, 2),
                       "algorithmic_bytes_per_launch": app_b,
                       "note": "64 rows per launch: latency-bound, not an HBM-bandwidth figure"},
     }
+    cpu = not args.no_cpu_baseline
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(torch, wl, shape, ctx, args.cpu_seconds)
     if not args.no_extras:
         del pools
         torch.cuda.empty_cache()
-        result["other_shapes"] = extra_measurements(torch, ops, wl, max(args.steps // 5, 5))
+        result["other_shapes"] = extra_measurements(torch, ops, wl, max(args.steps // 5, 5),
+                                                    cpu_budget=3.0, cpu=cpu)
     if not args.no_e2e:
-        result.setdefault("other_shapes", {})["qwen2_0.5b_e2e_continuous_batching"] = \
-            e2e_measurement(torch, args.e2e_seconds)
-    if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(torch, wl, shape, ctx, args.cpu_seconds)
+        e2e_res = e2e_measurement(torch, args.e2e_seconds)
+        if cpu:
+            e2e_res["cpu_baseline"] = e2e_cpu_subset(torch)
+        result.setdefault("other_shapes", {})["qwen2_0.5b_e2e_continuous_batching"] = e2e_res
     print(json.dumps(result), flush=True)
 
 
