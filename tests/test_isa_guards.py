@@ -24,8 +24,9 @@ def test_prefill_kernels_use_m0_only_for_direct_lds_loads(tmp_path):
                            "-I" + os.path.join(ROOT, "include"), "-S", "--cuda-device-only",
                            src, "-o", str(asm)], stderr=subprocess.DEVNULL)
     lines = asm.read_text().splitlines()
-    kernels = [i for i, l in enumerate(lines) if re.match(r"_ZN3ndl21varlen_prefill_kernel.*:", l)]
-    assert kernels
+    kernels = [i for i, l in enumerate(lines)
+               if re.match(r"_ZN3ndl(21varlen_prefill_kernel|24varlen_prefill_ws_kernel).*:", l)]
+    assert len(kernels) == 4
     for start in kernels:
         end = next(i for i in range(start, len(lines)) if lines[i].startswith(".Lfunc_end"))
         body = [l.strip() for l in lines[start:end] if not l.strip().startswith(";")]
