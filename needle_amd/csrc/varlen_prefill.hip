@@ -7,10 +7,14 @@
 // is the same data when context_lens == 0 and also covers a cached prefix.
 //
 // Design:
-//   * One workgroup = one (sequence, kv head, 32-row query tile).  Its waves are
-//     the query heads of the GQA group (times 32-row subtiles when the group is
-//     small), so every K/V tile staged in LDS serves all g heads, and every wave
-//     of a workgroup has the same causal extent.
+//   * The work of one (sequence, kv head) is a list of jobs, one per (query head of
+//     the GQA group, 32-row query subtile), subtile-major: job j is head j % g of
+//     subtile j / g.  A workgroup runs eight consecutive jobs, one per wave, so every
+//     K/V tile staged in LDS serves eight jobs and each of the four SIMDs carries two
+//     busy waves whatever g is (with one job per head, g = 7 would leave a SIMD half
+//     idle).  The eight jobs span one or two subtiles when g >= 7 (more for smaller
+//     groups); the workgroup walks the keys up to its last subtile's end and each
+//     wave masks past its own rows.
 //   * K/V advance 32 keys (two cache blocks) per step through an NS-stage LDS ring
 //     filled by direct global->LDS loads (global_load_lds_dwordx4, no register
 //     staging); each instruction reads whole rows, 1 KiB contiguous, and lands
@@ -36,18 +40,13 @@
 //     depend on nothing else in it, then the ring upkeep, masking and softmax.
 //   * Causal masking only on steps that reach past a wave's first query position;
 //     query tiles are dispatched longest-first.
-#include <stdlib.h>
-
-#include <type_traits>
-
 #include "ndl_common.hpp"
 
 namespace ndl {
 
 constexpr int kPrefKeys = 32;          // keys per step (two cache blocks)
 constexpr int kPrefRows = 32;          // query rows per wave
-constexpr int kPrefMaxWaves = 8;       // waves per workgroup
-constexpr int kPrefLoaders = 4;        // waves that issue the ring's direct loads
+constexpr int kPrefWaves = 8;          // waves (jobs) per workgroup
 // Tile-list limits of the persistent launch (larger batches use one workgroup per tile).
 constexpr int kPrefListSeqs = 8192;
 constexpr int kPrefListLevels = 2048;
@@ -73,9 +72,6 @@ struct PrefillArgs {
   const int32_t* context_lens;
   int num_heads;
   int group;          // query heads per kv head
-  int heads_per_wg;   // query heads one workgroup covers (a chunk of the group)
-  int head_chunks;    // workgroups per kv head along the group
-  int subtiles;       // 32-row subtiles per workgroup
   float scale_log2;
   int num_qtiles;
   int64_t num_tokens;
@@ -83,12 +79,12 @@ struct PrefillArgs {
   int persistent;     // 1: grid of resident workgroups walking the tile list
 };
 
-// One query tile, looked up one tile ahead by the persistent walk: rows
-// qtile * wg_rows .. of sequence seq, kv head kvh, head chunk chunk, with the sequence's
-// cu_seqlens pair and context length as loaded (checked where they are used, so that
-// the look-up does not wait for the loads).  seq < 0: no tile.
+// One workgroup tile, looked up one tile ahead by the persistent walk: jobs
+// 8 qtile .. 8 qtile + 7 of sequence seq, kv head kvh, with the sequence's cu_seqlens
+// pair and context length as loaded (checked where they are used, so that the look-up
+// does not wait for the loads).  seq < 0: no tile.
 struct PrefTile {
-  int seq, qtile, kvh, chunk;
+  int seq, qtile, kvh;
   int tok0, tok1, ctx;
 };
 
@@ -149,6 +145,20 @@ __device__ __forceinline__ int pref_swz(int r) {
   return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
 }
 
+// A compile-time int as a type, for the unrolled ring turn below.
+template <int N>
+struct Ic {
+  static constexpr int value = N;
+};
+// f(Ic<J>{}) for J = J0 .. N-1 in order.
+template <int J0, int N, class F>
+__device__ __forceinline__ void unroll(F& f) {
+  if constexpr (J0 < N) {
+    f(Ic<J0>{});
+    unroll<J0 + 1, N>(f);
+  }
+}
+
 // Combine a value with the one held by lane l ^ 32 (v_permlane32_swap of a register
 // with itself: one result holds the lower half's values, the other the upper half's).
 __device__ __forceinline__ float half_max(float v) {
@@ -163,16 +173,16 @@ __device__ __forceinline__ float half_sum(float v) {
 }
 
 template <int D, int NS>
-__global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(PrefillArgs a) {
   constexpr int KS = D / 16;          // k-steps of the QK MFMA (16 head_dim each)
   constexpr int DT = D / 32;          // 32-wide head_dim tiles of O^T
   constexpr int CPR = D / 8;          // 16-byte chunks per row
   constexpr int RPP = 512 / D;        // rows per 1 KiB piece (one direct load)
   constexpr int PIECES = kPrefKeys / RPP;                 // pieces per plane per step
-  constexpr int IPW = 2 * PIECES / kPrefLoaders;          // loads per loader wave per step
-  static_assert(IPW >= 1 && (2 * PIECES) % kPrefLoaders == 0, "load distribution");
+  constexpr int IPW = 2 * PIECES / kPrefWaves;            // direct loads per wave per step
+  static_assert(IPW >= 1 && (2 * PIECES) % kPrefWaves == 0, "load distribution");
   static_assert(NS >= 5 && NS - 3 <= 6 && (NS - 3) * IPW < 64, "ring depth");
-  static_assert(2 * NS - 3 >= kPrefMaxWaves, "an output piece per wave");
+  static_assert(2 * NS - 3 >= kPrefWaves, "an output piece per wave");
 
   // Ring of NS steps; each stage holds 32 K rows and 32 V rows.
   __shared__ __attribute__((aligned(16))) u16 lk[NS][kPrefKeys * D];
@@ -181,22 +191,25 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
-  const int hw = wave % a.heads_per_wg;                        // head within the chunk
-  const int sub = wave / a.heads_per_wg;                       // 32-row subtile
   const int r32 = lane & 31, h = lane >> 5;
-  const int wg_rows = kPrefRows * a.subtiles;
 
-  auto look_up = [&](int seq, int qtile, int kvh, int chunk) {
-    return PrefTile{seq, qtile, kvh, chunk, a.cu_seqlens[seq], a.cu_seqlens[seq + 1],
-                    a.context_lens[seq]};
+  // The look-up reads through the scalar cache (constant address space; the kernel never
+  // writes these arrays): its waits count scalar loads only and never drain the ring's
+  // direct loads.
+  typedef const __attribute__((address_space(4))) int32_t* cptr;
+  auto look_up = [&](int seq, int qtile, int kvh) {
+    const cptr cu = (cptr)a.cu_seqlens, cl = (cptr)a.context_lens;
+    return PrefTile{seq, qtile, kvh, cu[seq], cu[seq + 1], cl[seq]};
   };
+  // First row of a tile's first job.
+  auto first_row = [&](int qtile) { return qtile * kPrefWaves / a.group * kPrefRows; };
   // A tile's first token, rows and cached tokens; false if it has no rows.  Rows past
   // num_tokens are never touched, whatever cu_seqlens holds.
   auto bounds = [&](const PrefTile& t, int64_t& tok0, int& n, int& ctx) {
     if (t.seq < 0) return false;
     tok0 = t.tok0;
     const int64_t tok1 = t.tok1 < a.num_tokens ? (int64_t)t.tok1 : a.num_tokens;
-    if (tok0 < 0 || tok1 <= tok0 || (int64_t)t.qtile * wg_rows >= tok1 - tok0) return false;
+    if (tok0 < 0 || tok1 <= tok0 || (int64_t)first_row(t.qtile) >= tok1 - tok0) return false;
     n = (int)(tok1 - tok0);
     ctx = t.ctx < 0 ? 0 : t.ctx;
     return true;
@@ -214,14 +227,18 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       return;
     }
     const int seq = t.seq, kvh = t.kvh;
-    const int hg = t.chunk * a.heads_per_wg + hw;                // head within the group
+    const int job0 = t.qtile * kPrefWaves;
+    const int job = job0 + wave;
+    const int sub = job / a.group;                               // this wave's subtile
+    const int hg = job - sub * a.group;                          // head within the group
     const int head = kvh * a.group + hg;
-    const int row0 = t.qtile * wg_rows;
-    const int kv_end = ctx + (row0 + wg_rows < n ? row0 + wg_rows : n);
+    const int row0 = job0 / a.group * kPrefRows;                 // the tile's first row
+    const int row_end = ((job0 + kPrefWaves - 1) / a.group + 1) * kPrefRows;
+    const int kv_end = ctx + (row_end < n ? row_end : n);
     const int nsteps = (kv_end + kPrefKeys - 1) / kPrefKeys;
 
-    const int wrow0 = row0 + sub * kPrefRows;                    // first row of this wave
-    const bool wave_active = wrow0 < n && hg < a.group && sub < a.subtiles;
+    const int wrow0 = sub * kPrefRows;                           // first row of this wave
+    const bool wave_active = wrow0 < n;
     const int qpos_min = ctx + wrow0;
     const int qpos = ctx + wrow0 + r32;                          // this lane's query position
 
@@ -240,55 +257,60 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     // B operand of S^T = K Q^T: lane l supplies Q[row l%32][16 s + 8 h .. + 8).
     bf16x8 qb[KS];
     {
+      // Unconditional loads (rows past the range read the tile's first row and are
+      // zeroed), so that no branch hides them from the compiler's load counting.
       const int row = wrow0 + r32;
       const bool ok = wave_active && row < n;
       const u16* qrow = a.q + (tok0 + (ok ? row : 0)) * a.q_tok_stride + (int64_t)head * D + 8 * h;
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        u32x4 w = ok ? ld16(qrow + 16 * s) : u32x4{0u, 0u, 0u, 0u};
-        qb[s] = __builtin_bit_cast(bf16x8, w);
+        const u32x4 w = ld16(qrow + 16 * s);
+        qb[s] = __builtin_bit_cast(bf16x8, ok ? w : u32x4{0u, 0u, 0u, 0u});
       }
     }
-    ahead();
-    // Retire the Q and table loads (and the previous tile's L2 warm-up loads) before the
-    // ring starts, so that no wait inside the loop has to cover them (the ring's own
-    // waits count only its direct loads).
-    vm_wait<0>();
+    // The Q loads stay in flight while the ring's first steps are issued: vector-memory
+    // loads complete in issue order, so the ring's wait for step 0 covers them (and the
+    // table window, and the previous tile's L2 warm-up loads).  Loads issued after a
+    // step's (window refills) only make a ring wait, which counts the direct loads
+    // issued after that step, wait longer, never shorter.
 
-    // Loader waves 0..3 stage, per step, plane (w >> 1) (K, V) of block (w & 1) of the
-    // step: IPW direct loads of 1 KiB each, into pieces (w & 1) * IPW + e of that plane.
+    // Every wave stages, per step, IPW of the PIECES / 2 pieces (1 KiB, one direct load
+    // each) that block ld_blk of the step holds in plane ld_plane (K, V): pieces
+    // ld_half * IPW + e of the block, so that no wave's issue time carries more loads
+    // than another's (the step ends at a barrier).
     //   K piece: RPP rows, row-major, LDS slot L%CPR of row L/CPR holding chunk
     //     (L%CPR) ^ swz(row).
-    //   V piece e: the block's 16 rows at head_dim 32 e .. +32 ([row][32 d], 64 bytes
+    //   V piece e of a block: its 16 rows at head_dim 32 e .. +32 ([row][32 d], 64 bytes
     //     per row): lane L -> row L/4, chunk 4 e + L%4.
-    const bool loader = wave < kPrefLoaders;
-    const int ld_plane = wave >> 1, ld_blk = wave & 1;
+    static_assert((PIECES / 2) % IPW == 0, "load distribution");
+    const int ld_plane = wave >> 2, ld_blk = (wave >> 1) & 1, ld_half = wave & 1;
     const u16* ld_head = (ld_plane ? a.vplane : a.kplane) + (int64_t)kvh * 16 * D;
     uint32_t ld_off[IPW];
 #pragma unroll
     for (int e = 0; e < IPW; ++e) {
+      const int pe = ld_half * IPW + e;                     // piece within the block
       if (ld_plane == 0) {
-        const int r0 = (ld_blk * IPW + e) * RPP;            // first row of the piece (stage)
+        const int r0 = (ld_blk * (PIECES / 2) + pe) * RPP;  // first row of the piece (stage)
         const int r = r0 + lane / CPR;
         ld_off[e] = (uint32_t)((((r0 & 15) + lane / CPR) * D +
                                 8 * ((lane % CPR) ^ pref_swz<D>(r))) * 2);
       } else {
-        ld_off[e] = (uint32_t)(((lane >> 2) * D + 32 * e + 8 * (lane & 3)) * 2);
+        ld_off[e] = (uint32_t)(((lane >> 2) * D + 32 * pe + 8 * (lane & 3)) * 2);
       }
     }
     const uint32_t lds_k0 = lds_addr(&lk[0][0]), lds_v0 = lds_addr(&lv[0][0]);
-    const uint32_t ld_lds = (ld_plane ? lds_v0 : lds_k0) + ld_blk * IPW * 1024;
+    const uint32_t ld_lds =
+        (ld_plane ? lds_v0 : lds_k0) + (ld_blk * (PIECES / 2) + ld_half * IPW) * 1024;
 
     auto clamp_col = [&](int col) { return col > a.max_blocks - 1 ? a.max_blocks - 1 : col; };
     // bit 2*stage + b: block b of that stage's step is not a valid id.  Every wave keeps
     // its own copy (all waves walk the same table window).
     uint32_t badbits = 0;
 
-    // Stage `step` into ring slot `stage`: note its block validity and, on loader waves,
-    // issue its direct loads.  An invalid block id reads block 0 instead (always mapped);
+    // Stage `step` into ring slot `stage`: note its block validity and issue this wave's
+    // direct loads of it.  An invalid block id reads block 0 instead (always mapped);
     // rows past the range read whatever the table maps them to.  The softmax masks both.
-    // A window of the table with no invalid id (the normal case) sets no bits, and then
-    // only the loader waves read block ids.
+    // A window of the table with no invalid id (the normal case) sets no bits.
     bool win_bad = __builtin_amdgcn_ballot_w64(lane < a.max_blocks && (uint32_t)btw >= nb32) != 0;
     auto stage_in = [&](int step, int stage) {
       const int c0 = clamp_col(2 * step), c1 = clamp_col(2 * step + 1);  // same 64-window
@@ -300,12 +322,10 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
                                               (uint32_t)btw >= nb32) != 0;
       }
       badbits &= ~(3u << (2 * stage));
-      if (!loader && !win_bad) return;
       const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane(btw, c0 - win0);
       const uint32_t b1 = (uint32_t)__builtin_amdgcn_readlane(btw, c1 - win0);
       if (win_bad)
         badbits |= ((b0 >= nb32 ? 1u : 0u) | (b1 >= nb32 ? 2u : 0u)) << (2 * stage);
-      if (!loader) return;
       const uint32_t b = ld_blk ? b1 : b0;
       const u16* base = ld_head + (int64_t)(b < nb32 ? b : 0u) * blk_stride;
       const uint32_t lds = ld_lds + (uint32_t)stage * (kPrefKeys * D * 2);
@@ -317,7 +337,6 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     // Waits until this wave's loads of the step after the current one have landed:
     // `later` = steps issued after it.
     auto wait_loads = [&](int later) {
-      if (!loader) return;
       switch (later) {
         case 0: vm_wait<0>(); break;
         case 1: vm_wait<IPW>(); break;
@@ -359,6 +378,23 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
       for (int s = 0; s < KS; ++s)
         st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[s]), qb[s], st,
                                                      0, 0, 0);
+      return st;
+    };
+    // The same product with the K operands read in two halves (fewer live registers).
+    auto qk_halves = [&](int stage) {
+      const u16* kt = lk[stage];
+      f32x16 st = {};
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        u32x4 ka[KS / 2];
+#pragma unroll
+        for (int s = 0; s < KS / 2; ++s)
+          ka[s] = *reinterpret_cast<const u32x4*>(&kt[koff[half * KS / 2 + s]]);
+#pragma unroll
+        for (int s = 0; s < KS / 2; ++s)
+          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[s]),
+                                                       qb[half * KS / 2 + s], st, 0, 0, 0);
+      }
       return st;
     };
     // P = exp2(s * scale log2e - m) rounded to bf16 (the B operand of the PV product);
@@ -444,7 +480,7 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     auto sync = [&](int step, int mode) {
       const int lead = step + (mode == kPair ? 2 : 1);
       const int need = lead < nsteps - 1 ? lead : nsteps - 1;
-      if (loader && need > step) {
+      if (need > step) {
         // steps issued at the barrier before this one, counted from `step`
         const int ahead = step + (mode == kSecond ? NS - 2 : NS - 3);
         const int later = (ahead < nsteps - 1 ? ahead : nsteps - 1) - need;
@@ -555,6 +591,7 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
 #pragma unroll
     for (int t = 0; t < NS - 2; ++t)
       if (t < nsteps) stage_in(t, t);
+    ahead();
     wait_loads(nsteps - 1 < NS - 3 ? nsteps - 1 : NS - 3);
     lds_barrier();
     if (needs_vzero(0, 0)) zero_v(0, 0);
@@ -582,7 +619,6 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
           stage_in(x, sl);
           return;
         }
-        if (!loader) return;
         const uint32_t b = (uint32_t)__builtin_amdgcn_readlane(btw, c0 + ld_blk - win0);
         const u16* base = ld_head + (int64_t)b * blk_stride;
         const uint32_t lds = ld_lds + (uint32_t)sl * (kPrefKeys * D * 2);
@@ -590,18 +626,16 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
         for (int e = 0; e < IPW; ++e)
           lds_dma16(base, ld_off[e], lds + 1024 * e);
       };
-      for (; step < lim && badbits == 0; step += 2) {
+      while (step < lim && badbits == 0) {
         const int stage1 = stage + 1 == NS ? 0 : stage + 1;
         const int stage2 = stage1 + 1 == NS ? 0 : stage1 + 1;
         // Loads of steps up to step + 2 (the last one at most) landed: steps issued after
         // it stay out, NS - 5 of them while the ring is in full flow.
-        if (loader) {
-          if (step + NS - 3 <= nsteps - 1) {
-            vm_wait<(NS - 5) * IPW>();
-          } else {
-            const int need = step + 2 < nsteps - 1 ? step + 2 : nsteps - 1;
-            wait_loads(nsteps - 1 - need);
-          }
+        if (step + NS - 3 <= nsteps - 1) {
+          vm_wait<(NS - 5) * IPW>();
+        } else {
+          const int need = step + 2 < nsteps - 1 ? step + 2 : nsteps - 1;
+          wait_loads(nsteps - 1 - need);
         }
         lds_barrier();
         u32x4 ka[KS];
@@ -618,6 +652,7 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
         st0 = qk(ka);
         finish(step + 1, stage1, st1, vop, false);
         stage = stage2;
+        step += 2;
       }
     }
 
@@ -637,9 +672,10 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     int64_t ntok0;
     int nn, nctx;
     if (bounds(nx, ntok0, nn, nctx)) {
-      const int nrow0 = nx.qtile * wg_rows + sub * kPrefRows;
-      const int nhg = nx.chunk * a.heads_per_wg + hw;
-      if (nrow0 < nn && nhg < a.group && sub < a.subtiles) {
+      const int njob = nx.qtile * kPrefWaves + wave;
+      const int nsub = njob / a.group, nhg = njob - nsub * a.group;
+      const int nrow0 = nsub * kPrefRows;
+      if (nrow0 < nn) {
         const int r = nrow0 + (lane >> 1) < nn ? lane >> 1 : 0;
         const u16* base = a.q + (ntok0 + nrow0) * a.q_tok_stride +
                           (int64_t)(nx.kvh * a.group + nhg) * D;
@@ -704,9 +740,8 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   };  // tile
 
   if (!a.persistent) {
-    tile(look_up(blockIdx.y, a.num_qtiles - 1 - (int)blockIdx.z, blockIdx.x / a.head_chunks,
-                 blockIdx.x % a.head_chunks),
-         PrefTile{-1, 0, 0, 0, 0, 0, 0}, [] {});
+    tile(look_up(blockIdx.y, a.num_qtiles - 1 - (int)blockIdx.z, blockIdx.x),
+         PrefTile{-1, 0, 0, 0, 0, 0}, [] {});
     return;
   }
 
@@ -718,7 +753,7 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
   __shared__ uint16_t s_ntiles[kPrefListSeqs];
   __shared__ int s_cnt[kPrefListLevels];    // sequences with more than t tiles
   __shared__ int s_off[kPrefListLevels];    // items in the levels above t
-  const int S = a.num_seqs, NQ = a.num_qtiles, KVC = a.num_kv_heads * a.head_chunks;
+  const int S = a.num_seqs, NQ = a.num_qtiles, KVC = a.num_kv_heads;
   for (int t = tid; t < NQ; t += blockDim.x) s_cnt[t] = 0;
   lds_barrier();
   for (int q = tid; q < S; q += blockDim.x) {
@@ -727,7 +762,8 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     if (t1 > a.num_tokens) t1 = a.num_tokens;
     int nt = 0;
     if (t0 >= 0 && t1 > t0) {
-      const int64_t x = (t1 - t0 + wg_rows - 1) / wg_rows;
+      const int64_t subs = (t1 - t0 + kPrefRows - 1) / kPrefRows;
+      const int64_t x = (subs * a.group + kPrefWaves - 1) / kPrefWaves;
       nt = x > NQ ? NQ : (int)x;
     }
     s_ntiles[q] = (uint16_t)nt;
@@ -800,7 +836,7 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
           rank -= pc;
         }
       }
-      out = look_up(seq, lvl, c / a.head_chunks, c % a.head_chunks);
+      out = look_up(seq, lvl, c);
       ++r;
       return true;
     }
@@ -817,610 +853,6 @@ __global__ __launch_bounds__(64 * kPrefMaxWaves) void varlen_prefill_kernel(Pref
     cur = nxt;
     have = more;
   }
-}
-
-// ---------------------------------------------------------------------------------------
-// Warp-specialized variant (the default; varlen_prefill_kernel above stays selectable).
-//
-// The same workgroup tile (sequence, kv head, 32-row query tiles of the group's heads), the
-// same K/V ring fed by direct global->LDS loads, the same MFMA operand layouts and softmax
-// arithmetic, but each (head, 32-row subtile) job is split over two waves:
-//   S wave: S^T = K Q^T (v_mfma_f32_32x32x16_bf16, Q^T in registers), causal mask, online
-//           softmax; writes P (bf16, the PV product's B operand, in its own lane order) and
-//           the step's row rescale factor to LDS;
-//   O wave: reads them back in the same lane order (so no shuffle), rescales its O^T
-//           accumulator when a row max moved, O^T += V^T P^T, and writes the output tile.
-// Each wave needs about half the registers of the combined job (<= 128: four waves per
-// SIMD, 16 per CU instead of 7), so one wave's exponentials overlap another's MFMAs.  The
-// S waves run one step ahead: in iteration i they issue QK of step i + 1, then the softmax
-// of step i; the O waves do PV of step i - 1.  One workgroup barrier per step:
-//   B(i) publishes K(i + 1) (its loads waited for in iteration i - 1), P(i - 1) and the
-//   V rows of step i - 1 cleared in iteration i - 2; it retires the O waves' reads of P(i - 2)
-//   (so the S waves may write P(i) into that buffer) and every read of step i - 2's slot,
-//   which the loaders refill with step i + NS - 2 in iteration i.
-// The last four waves (O waves) issue the ring's loads and clear V rows past the range.
-constexpr int kWsMaxPairs = 8;                 // (S, O) wave pairs per workgroup
-constexpr int kWsListSeqs = 2048;              // persistent-walk table limits
-constexpr int kWsListLevels = 1024;
-
-template <int D, int NS>
-__global__ __launch_bounds__(64 * 2 * kWsMaxPairs) void varlen_prefill_ws_kernel(PrefillArgs a) {
-  constexpr int KS = D / 16;          // k-steps of the QK MFMA (16 head_dim each)
-  constexpr int DT = D / 32;          // 32-wide head_dim tiles of O^T
-  constexpr int CPR = D / 8;          // 16-byte chunks per row
-  constexpr int RPP = 512 / D;        // rows per 1 KiB piece (one direct load)
-  constexpr int PIECES = kPrefKeys / RPP;                 // pieces per plane per step
-  constexpr int IPW = 2 * PIECES / kPrefLoaders;          // loads per loader wave per step
-  static_assert(IPW >= 1 && (2 * PIECES) % kPrefLoaders == 0, "load distribution");
-  static_assert(NS >= 6 && (NS - 3) * IPW < 64, "ring depth");
-  static_assert(2 * NS - 1 >= kWsMaxPairs, "an output plane per O wave");
-
-  __shared__ __attribute__((aligned(16))) u16 lk[NS][kPrefKeys * D];
-  __shared__ __attribute__((aligned(16))) u16 lv[NS][kPrefKeys * D];
-  // P of one step per pair, two steps deep: word 4 * (64 q + lane) + e holds the lane's
-  // P word 4 q + e (q = 0, 1), so each lane's 16-byte accesses are contiguous across lanes.
-  __shared__ __attribute__((aligned(16))) uint32_t pbuf[2][kWsMaxPairs][8 * 64];
-  __shared__ float abuf[2][kWsMaxPairs][64];    // the step's rescale factor per lane (row)
-  __shared__ float lbuf[kWsMaxPairs][64];       // the tile's row sums per lane
-  __shared__ uint32_t lds_sink[64];             // destination of the L2 warm-up loads
-
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nwaves = __builtin_amdgcn_readfirstlane((int)(blockDim.x >> 6));
-  const int pairs = nwaves >> 1;
-  const bool s_wave = wave < pairs;
-  const int pr = s_wave ? wave : wave - pairs;                 // the job of this pair
-  const int hw = pr % a.heads_per_wg;                          // head within the chunk
-  const int sub = pr / a.heads_per_wg;                         // 32-row subtile
-  const int r32 = lane & 31, h = lane >> 5;
-  const int wg_rows = kPrefRows * a.subtiles;
-  const bool loader = wave >= nwaves - kPrefLoaders;
-  const int lw = wave - (nwaves - kPrefLoaders);               // 0..3 on loader waves
-
-  auto look_up = [&](int seq, int qtile, int kvh, int chunk) {
-    return PrefTile{seq, qtile, kvh, chunk, a.cu_seqlens[seq], a.cu_seqlens[seq + 1],
-                    a.context_lens[seq]};
-  };
-  auto bounds = [&](const PrefTile& t, int64_t& tok0, int& n, int& ctx) {
-    if (t.seq < 0) return false;
-    tok0 = t.tok0;
-    const int64_t tok1 = t.tok1 < a.num_tokens ? (int64_t)t.tok1 : a.num_tokens;
-    if (tok0 < 0 || tok1 <= tok0 || (int64_t)t.qtile * wg_rows >= tok1 - tok0) return false;
-    n = (int)(tok1 - tok0);
-    ctx = t.ctx < 0 ? 0 : t.ctx;
-    return true;
-  };
-
-  // `role` (std::integral_constant<bool, S>) makes each role its own instantiation of the
-  // tile and of the walk below: the roles split once, at the top of the kernel, so the
-  // register allocator never sees the S waves' Q operands and scores live together with
-  // the O waves' accumulators.
-  auto tile = [&](auto role, const PrefTile& t, const PrefTile& nx, auto&& ahead) {
-    constexpr bool kS = decltype(role)::value;
-    int64_t tok0;
-    int n, ctx;
-    if (!bounds(t, tok0, n, ctx)) {
-      ahead();
-      return;
-    }
-    const int seq = t.seq, kvh = t.kvh;
-    const int hg = t.chunk * a.heads_per_wg + hw;                // head within the group
-    const int head = kvh * a.group + hg;
-    const int row0 = t.qtile * wg_rows;
-    const int kv_end = ctx + (row0 + wg_rows < n ? row0 + wg_rows : n);
-    const int nsteps = (kv_end + kPrefKeys - 1) / kPrefKeys;
-
-    const int wrow0 = row0 + sub * kPrefRows;                    // first row of this job
-    const bool job_active = wrow0 < n && hg < a.group && sub < a.subtiles;
-    const int qpos_min = ctx + wrow0;
-
-    const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
-    const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
-    const uint32_t nb32 = a.num_blocks > 0x7fffffff ? 0x80000000u : (uint32_t)a.num_blocks;
-    int win0 = 0;
-    int btw = lane < a.max_blocks ? bt_row[lane] : 0;
-
-    // S waves: B operand of S^T = K Q^T, lane l supplies Q[row l%32][16 s + 8 h .. + 8).
-    bf16x8 qb[KS];
-    if constexpr (kS) {
-      const int row = wrow0 + r32;
-      const bool ok = job_active && row < n;
-      const u16* qrow = a.q + (tok0 + (ok ? row : 0)) * a.q_tok_stride + (int64_t)head * D + 8 * h;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        u32x4 w = ok ? ld16(qrow + 16 * s) : u32x4{0u, 0u, 0u, 0u};
-        qb[s] = __builtin_bit_cast(bf16x8, w);
-      }
-    }
-    ahead();
-    vm_wait<0>();
-
-    // Loader lw stages plane (lw >> 1) of block (lw & 1) of each step (layouts as in
-    // varlen_prefill_kernel).
-    const int ld_plane = lw >> 1, ld_blk = lw & 1;
-    const u16* ld_head = (ld_plane ? a.vplane : a.kplane) + (int64_t)kvh * 16 * D;
-    // Lane offset of load e within the block (recomputed at each use: a few VALU instead of
-    // registers held through both loops).
-    auto ld_off = [&](int e) {
-      if (ld_plane == 0) {
-        const int r0 = (ld_blk * IPW + e) * RPP;
-        const int r = r0 + lane / CPR;
-        return (uint32_t)((((r0 & 15) + lane / CPR) * D + 8 * ((lane % CPR) ^ pref_swz<D>(r))) * 2);
-      }
-      return (uint32_t)(((lane >> 2) * D + 32 * e + 8 * (lane & 3)) * 2);
-    };
-    const uint32_t lds_k0 = lds_addr(&lk[0][0]), lds_v0 = lds_addr(&lv[0][0]);
-    const uint32_t ld_lds = (ld_plane ? lds_v0 : lds_k0) + ld_blk * IPW * 1024;
-
-    auto clamp_col = [&](int col) { return col > a.max_blocks - 1 ? a.max_blocks - 1 : col; };
-    uint32_t badbits = 0;   // bit 2 * slot + b: block b of that slot's step is invalid
-    bool win_bad = __builtin_amdgcn_ballot_w64(lane < a.max_blocks && (uint32_t)btw >= nb32) != 0;
-    auto stage_in = [&](int step, int stage) {
-      const int c0 = clamp_col(2 * step), c1 = clamp_col(2 * step + 1);
-      if (c0 < win0 || c0 >= win0 + 64) {
-        win0 = c0 & ~63;
-        btw = win0 + lane < a.max_blocks ? bt_row[win0 + lane] : 0;
-        vm_wait<0>();
-        win_bad = __builtin_amdgcn_ballot_w64(win0 + lane < a.max_blocks &&
-                                              (uint32_t)btw >= nb32) != 0;
-      }
-      badbits &= ~(3u << (2 * stage));
-      if (!loader && !win_bad) return;
-      const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane(btw, c0 - win0);
-      const uint32_t b1 = (uint32_t)__builtin_amdgcn_readlane(btw, c1 - win0);
-      if (win_bad)
-        badbits |= ((b0 >= nb32 ? 1u : 0u) | (b1 >= nb32 ? 2u : 0u)) << (2 * stage);
-      if (!loader) return;
-      const uint32_t b = ld_blk ? b1 : b0;
-      const u16* base = ld_head + (int64_t)(b < nb32 ? b : 0u) * blk_stride;
-      const uint32_t lds = ld_lds + (uint32_t)stage * (kPrefKeys * D * 2);
-#pragma unroll
-      for (int e = 0; e < IPW; ++e)
-        lds_dma16(base, ld_off(e), lds + 1024 * e);
-    };
-    // Loader waves: wait until the loads of a step have landed; `later` = steps issued
-    // after it.
-    auto wait_loads = [&](int later) {
-      if (!loader) return;
-      switch (later) {
-        case 0: vm_wait<0>(); break;
-        case 1: vm_wait<IPW>(); break;
-        case 2: vm_wait<2 * IPW>(); break;
-        case 3: vm_wait<3 * IPW>(); break;
-        case 4: vm_wait<4 * IPW>(); break;
-        case 5: vm_wait<5 * IPW>(); break;
-        default: vm_wait<6 * IPW>(); break;
-      }
-    };
-    auto slot_of = [](int step) { return step % NS; };
-
-    auto probs = [&](const f32x16& st, float m_use, uint32_t* pw, float& lsum) {
-#pragma unroll
-      for (int r = 0; r < 16; r += 2) {
-        const float p0 = fast_exp2(fmaf(st[r], a.scale_log2, -m_use));
-        const float p1 = fast_exp2(fmaf(st[r + 1], a.scale_log2, -m_use));
-        pw[r >> 1] = pack_bf16x2(p0, p1);
-        lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[r >> 1]),
-                                               bf16x2{(__bf16)1.0f, (__bf16)1.0f}, lsum, false);
-      }
-    };
-    auto needs_vzero = [&](int step, int stage) {
-      return step * kPrefKeys + kPrefKeys > kv_end || ((badbits >> (2 * stage)) & 3u) != 0;
-    };
-    // Loader waves clear the V rows of a step that lie past the range or in an invalid block
-    // (NaN * 0 = NaN in the PV product).
-    auto zero_v = [&](int step, int stage) {
-      const int kv0 = step * kPrefKeys;
-      int valid[2];
-#pragma unroll
-      for (int t2 = 0; t2 < 2; ++t2) {
-        const int v = (badbits >> (2 * stage + t2)) & 1u ? 0 : kv_end - (kv0 + 16 * t2);
-        valid[t2] = v < 0 ? 0 : (v > 16 ? 16 : v);
-      }
-      for (int c = lw * 64 + lane; c < 2 * DT * 64; c += 64 * kPrefLoaders) {
-        const int piece = c >> 6, row = (c & 63) >> 2;
-        if (row >= valid[piece / DT]) st16(&lv[stage][c * 8], u32x4{0u, 0u, 0u, 0u});
-      }
-    };
-
-    const int pb = pr * 8 * 64;   // this pair's P words within a buffer
-
-    // Ring upkeep of iteration i, run by every wave after its work of the iteration (the
-    // block-id bookkeeping on all waves, the loads, V clearing and waits on the loaders).
-    auto upkeep = [&](int i) {
-      if (i + NS - 2 < nsteps) stage_in(i + NS - 2, slot_of(i + NS - 2));
-      if (loader && i + 1 < nsteps && needs_vzero(i + 1, slot_of(i + 1)))
-        zero_v(i + 1, slot_of(i + 1));
-      if (i + 2 < nsteps) {
-        const int last = i + NS - 2 < nsteps - 1 ? i + NS - 2 : nsteps - 1;
-        wait_loads(last - (i + 2));              // step i + 2 landed before B(i + 1)
-      }
-    };
-
-    // Ring start: the barrier retires every wave's reads of the previous tile.
-    lds_barrier();
-    const int first_batch = nsteps - 1 < NS - 3 ? nsteps - 1 : NS - 3;
-    for (int s0 = 0; s0 <= first_batch; ++s0) stage_in(s0, s0);
-    wait_loads(first_batch);                     // step 0 landed
-    lds_barrier();                               // B(-1) publishes step 0
-    if (loader && needs_vzero(0, 0)) zero_v(0, 0);
-    if (nsteps > 1) wait_loads(first_batch - 1); // step 1 landed before B(0)
-
-    // The two roles run separate loops with the same barrier sequence.
-    if constexpr (kS) {
-      const int qpos = ctx + wrow0 + r32;      // this lane's query position
-      // K operand of k-step s: row r32, chunk (2 s + h) ^ swz(r32) = 2 s ^ kx (2 s has bit 0
-      // clear), computed per read from two registers instead of KS offsets kept live.
-      const int kbase = r32 * D, kx = h ^ pref_swz<D>(r32);
-      // S^T of one step: K operands read from LDS in two halves, each right before its MFMAs
-      // (four operands in flight instead of eight).
-      auto qk_step = [&](int stage) {
-        const u16* kt = lk[stage];
-        f32x16 st = {};
-#pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          u32x4 ka[KS / 2];
-#pragma unroll
-          for (int s = 0; s < KS / 2; ++s)
-            ka[s] = *reinterpret_cast<const u32x4*>(
-                &kt[kbase + 8 * ((2 * (half * (KS / 2) + s)) ^ kx)]);
-#pragma unroll
-          for (int s = 0; s < KS / 2; ++s)
-            st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[s]),
-                                                         qb[half * (KS / 2) + s], st, 0, 0, 0);
-          __builtin_amdgcn_sched_barrier(0);   // the next half's reads stay below
-        }
-        return st;
-      };
-      float m_run = kNegInf;   // running max of this lane's row (exp2 domain)
-      float l_run = 0.f;       // this lane's share of the row sum
-      // Step `step`: mask, softmax, P and the rescale factor to LDS.
-      auto softmax_step = [&](int step, int stage, f32x16 st) {
-        const int kv0 = step * kPrefKeys;
-        const bool masked = kv0 + kPrefKeys - 1 > qpos_min || kv0 + kPrefKeys > kv_end ||
-                            ((badbits >> (2 * stage)) & 3u) != 0;
-        if (masked) {
-          const bool bad0 = (badbits >> (2 * stage)) & 1u;
-          const bool bad1 = (badbits >> (2 * stage + 1)) & 1u;
-#pragma unroll
-          for (int r = 0; r < 16; ++r) {
-            const int key = 8 * (r >> 2) + 4 * h + (r & 3);
-            const int kp = kv0 + key;
-            const bool ok = kp <= qpos && kp < kv_end && !(key < 16 ? bad0 : bad1);
-            st[r] = ok ? st[r] : kNegInf;
-          }
-        }
-        uint32_t pw[8];
-        float lstep = 0.f;
-        float alpha = 1.f;
-        probs(st, m_run == kNegInf ? 0.f : m_run, pw, lstep);
-        const bool exact = !(lstep <= kGrowSum) || m_run == kNegInf;
-        if (__builtin_amdgcn_ballot_w64(exact) != 0) {
-          float m3[6];
-#pragma unroll
-          for (int i = 0; i < 5; ++i) m3[i] = fmaxf(fmaxf(st[3 * i], st[3 * i + 1]), st[3 * i + 2]);
-          m3[5] = st[15];
-          float mx = fmaxf(fmaxf(fmaxf(m3[0], m3[1]), m3[2]), fmaxf(fmaxf(m3[3], m3[4]), m3[5]));
-          mx = half_max(mx);
-          const float m_new = fmaxf(m_run, mx * a.scale_log2);
-          if (m_new != m_run) {
-            alpha = fast_exp2(m_run - m_new);   // 0 while nothing is accumulated
-            l_run *= alpha;
-            m_run = m_new;
-          }
-          lstep = 0.f;
-          probs(st, m_run == kNegInf ? 0.f : m_run, pw, lstep);
-        }
-        l_run += lstep;
-        uint32_t* dst = &pbuf[step & 1][0][0] + pb;
-        *reinterpret_cast<u32x4*>(dst + 4 * lane) = u32x4{pw[0], pw[1], pw[2], pw[3]};
-        *reinterpret_cast<u32x4*>(dst + 4 * (64 + lane)) = u32x4{pw[4], pw[5], pw[6], pw[7]};
-        abuf[step & 1][pr][lane] = alpha;
-      };
-      for (int i = 0; i <= nsteps; ++i) {
-        lds_barrier();                           // B(i)
-        if (i < nsteps && job_active) {
-          softmax_step(i, slot_of(i), qk_step(slot_of(i)));
-          if (i == nsteps - 1) lbuf[pr][lane] = half_sum(l_run);
-        }
-        upkeep(i);
-      }
-    } else {
-      const int vlane =
-          (4 * h + ((lane & 15) >> 2)) * 32 + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    // V^T operands of one 16-key half (t2) of a step: DT transpose-read pairs.
-      auto v_reads = [&](int stage, int t2, bf16x8* vop) {
-        const u16* vt = lv[stage] + vlane;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt) {
-          const u16* piece = vt + (t2 * DT + dt) * 512;
-          const i16x4v v0 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) i16x4v*)(piece));
-          const i16x4v v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) i16x4v*)(piece + 8 * 32));
-          const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
-          vop[dt] = __builtin_bit_cast(bf16x8, u32x4{w0[0], w0[1], w1[0], w1[1]});
-        }
-      };
-      f32x16 acc[DT];
-#pragma unroll
-      for (int t2 = 0; t2 < DT; ++t2) acc[t2] = f32x16{};
-      // Step `step`: rescale when a row max moved, O^T += V^T P^T.
-      auto pv_step = [&](int step, int stage) {
-        const uint32_t* src = &pbuf[step & 1][0][0] + pb;
-        const u32x4 p0 = *reinterpret_cast<const u32x4*>(src + 4 * lane);
-        const u32x4 p1 = *reinterpret_cast<const u32x4*>(src + 4 * (64 + lane));
-        const float alpha = abuf[step & 1][pr][lane];
-        bf16x8 vop[DT];
-        v_reads(stage, 0, vop);
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.f) != 0) {
-#pragma unroll
-          for (int t2 = 0; t2 < DT; ++t2) acc[t2] *= alpha;
-        }
-#pragma unroll
-        for (int t2 = 0; t2 < 2; ++t2) {
-          if (t2 == 1) {
-            __builtin_amdgcn_sched_barrier(0);   // the second half's reads stay below
-            v_reads(stage, 1, vop);
-          }
-          const bf16x8 pbv = __builtin_bit_cast(bf16x8, t2 == 0 ? p0 : p1);
-#pragma unroll
-          for (int dt = 0; dt < DT; ++dt)
-            acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[dt], pbv, acc[dt], 0, 0, 0);
-        }
-      };
-      for (int i = 0; i <= nsteps; ++i) {
-        lds_barrier();                           // B(i)
-        if (i >= 1 && job_active) pv_step(i - 1, slot_of(i - 1));
-        upkeep(i);
-      }
-      if (job_active) {
-        // Normalise and store.  The tile (32 rows x D) goes through an LDS plane nothing
-        // reads any more: every K plane (the S waves read the last one before B(nsteps)),
-        // or a V plane other than step nsteps - 1's, which other O waves may still read.
-        const float l = lbuf[pr][lane];
-        const float inv = l > 0.f ? 1.f / l : 0.f;
-        u16* piece = pr < NS ? lk[pr] : lv[(nsteps + (pr - NS)) % NS];
-        int ln = lane;
-        asm volatile("" : "+v"(ln));
-        const int rr = ln & 31, hh = ln >> 5;
-#pragma unroll
-        for (int dt = 0; dt < DT; ++dt)
-#pragma unroll
-          for (int b = 0; b < 4; ++b)
-            *reinterpret_cast<u32x2*>(piece + rr * D + 8 * ((4 * dt + b) ^ (rr % CPR)) + 4 * hh) =
-                u32x2{pack_bf16x2(acc[dt][4 * b] * inv, acc[dt][4 * b + 1] * inv),
-                      pack_bf16x2(acc[dt][4 * b + 2] * inv, acc[dt][4 * b + 3] * inv)};
-        __builtin_amdgcn_wave_barrier();
-        constexpr int RPI = 64 / CPR;
-        const int c = ln % CPR;
-        u32x4 ov[32 / RPI];
-#pragma unroll
-        for (int i = 0; i < 32 / RPI; ++i) {
-          const int r = RPI * i + ln / CPR;
-          ov[i] = *reinterpret_cast<const u32x4*>(piece + r * D + 8 * (c ^ (r % CPR)));
-        }
-        u16* dst = a.out + ((tok0 + wrow0 + ln / CPR) * a.num_heads + head) * (int64_t)D + 8 * c;
-        const int64_t rstride = (int64_t)RPI * a.num_heads * D;
-        if (wrow0 + 32 <= n) {
-#pragma unroll
-          for (int i = 0; i < 32 / RPI; ++i) *reinterpret_cast<u32x4*>(dst + i * rstride) = ov[i];
-        } else {
-#pragma unroll
-          for (int i = 0; i < 32 / RPI; ++i)
-            if (wrow0 + RPI * i + ln / CPR < n)
-              *reinterpret_cast<u32x4*>(dst + i * rstride) = ov[i];
-        }
-      }
-    }
-
-    // Pull the next tile's Q rows (S waves) and table window (wave 0) into the L2.
-    int64_t ntok0;
-    int nn, nctx;
-    if (bounds(nx, ntok0, nn, nctx)) {
-      const int nrow0 = nx.qtile * wg_rows + sub * kPrefRows;
-      const int nhg = nx.chunk * a.heads_per_wg + hw;
-      if (kS && nrow0 < nn && nhg < a.group && sub < a.subtiles) {
-        const int r = nrow0 + (lane >> 1) < nn ? lane >> 1 : 0;
-        const u16* base = a.q + (ntok0 + nrow0) * a.q_tok_stride +
-                          (int64_t)(nx.kvh * a.group + nhg) * D;
-        lds_dma4(base, (uint32_t)(r * a.q_tok_stride * 2) + (D >= 128 ? (lane & 1) * 128u : 0u),
-                 lds_addr(lds_sink));
-      }
-      if (wave == 0)
-        lds_dma4(a.block_table + (int64_t)nx.seq * a.bt_row_stride,
-                 4u * (uint32_t)(lane < a.max_blocks ? lane : a.max_blocks - 1), lds_addr(lds_sink));
-    }
-  };  // tile
-
-  if (!a.persistent) {
-    const PrefTile only = look_up(blockIdx.y, a.num_qtiles - 1 - (int)blockIdx.z,
-                                  blockIdx.x / a.head_chunks, blockIdx.x % a.head_chunks);
-    if (s_wave)
-      tile(std::true_type{}, only, PrefTile{-1, 0, 0, 0, 0, 0, 0}, [] {});
-    else
-      tile(std::false_type{}, only, PrefTile{-1, 0, 0, 0, 0, 0, 0}, [] {});
-    return;
-  }
-
-  // Persistent launch: the longest-first tile list and snake deal of varlen_prefill_kernel.
-  __shared__ uint16_t s_ntiles[kWsListSeqs];
-  __shared__ int s_cnt[kWsListLevels];
-  __shared__ int s_off[kWsListLevels];
-  const int S = a.num_seqs, NQ = a.num_qtiles, KVC = a.num_kv_heads * a.head_chunks;
-  for (int t = tid; t < NQ; t += blockDim.x) s_cnt[t] = 0;
-  lds_barrier();
-  for (int q = tid; q < S; q += blockDim.x) {
-    const int64_t t0 = a.cu_seqlens[q];
-    int64_t t1 = a.cu_seqlens[q + 1];
-    if (t1 > a.num_tokens) t1 = a.num_tokens;
-    int nt = 0;
-    if (t0 >= 0 && t1 > t0) {
-      const int64_t x = (t1 - t0 + wg_rows - 1) / wg_rows;
-      nt = x > NQ ? NQ : (int)x;
-    }
-    s_ntiles[q] = (uint16_t)nt;
-    if (nt > 0) atomicAdd(&s_cnt[nt - 1], 1);
-  }
-  lds_barrier();
-  if (wave == 0) {
-    int run_cnt = 0, run_items = 0;
-    for (int base = NQ - 1; base >= 0; base -= 64) {
-      const int t = base - lane;
-      const int hcount = t >= 0 ? s_cnt[t] : 0;
-      int inc = hcount;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(inc, d, 64);
-        if (lane >= d) inc += o;
-      }
-      const int cnt = run_cnt + inc;
-      int inc_items = cnt;
-#pragma unroll
-      for (int d = 1; d < 64; d <<= 1) {
-        const int o = __shfl_up(inc_items, d, 64);
-        if (lane >= d) inc_items += o;
-      }
-      if (t >= 0) {
-        s_cnt[t] = cnt;
-        s_off[t] = (run_items + inc_items - cnt) * KVC;
-      }
-      run_cnt = __shfl(cnt, 63, 64);
-      run_items += __shfl(inc_items, 63, 64);
-    }
-  }
-  lds_barrier();
-  const int total = NQ > 0 ? s_off[0] + s_cnt[0] * KVC : 0;
-  const int G = gridDim.x, w = blockIdx.x;
-  int lvl = NQ - 1;
-  int r = 0;
-  auto next_item = [&](PrefTile& out) {
-    for (; r * G < total; ++r) {
-      const int j = (r & 1) ? r * G + (G - 1 - w) : r * G + w;
-      if (j >= total) continue;
-      for (;;) {
-        const int t = lvl - lane;
-        const uint64_t m = __builtin_amdgcn_ballot_w64(t >= 0 && j < s_off[t] + s_cnt[t] * KVC);
-        if (m != 0) {
-          lvl -= __builtin_ctzll(m);
-          break;
-        }
-        lvl -= 64;
-      }
-      const int i = j - s_off[lvl];
-      int rank = i / KVC;
-      const int c = i - rank * KVC;
-      int seq = -1;
-      for (int base = 0; base < S && seq < 0; base += 64) {
-        const int q = base + lane;
-        const bool has = q < S && s_ntiles[q] > lvl;
-        const uint64_t m = __builtin_amdgcn_ballot_w64(has);
-        const int pc = __builtin_popcountll(m);
-        if (rank < pc) {
-          const int below = (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32),
-                                                          __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0));
-          seq = base + __builtin_ctzll(__builtin_amdgcn_ballot_w64(has && below == rank));
-        } else {
-          rank -= pc;
-        }
-      }
-      out = look_up(seq, lvl, c / a.head_chunks, c % a.head_chunks);
-      ++r;
-      return true;
-    }
-    return false;
-  };
-  auto walk = [&](auto role) {
-    PrefTile cur, nxt;
-    bool have = next_item(cur), more = false;
-    while (have) {
-      tile(role, cur, nxt, [&] {
-        more = next_item(nxt);
-        if (!more) nxt.seq = -1;
-      });
-      cur = nxt;
-      have = more;
-    }
-  };
-  if (s_wave)
-    walk(std::true_type{});
-  else
-    walk(std::false_type{});
-}
-
-
-// Which prefill kernel runs: varlen_prefill_kernel by default; NDL_PREFILL_IMPL=split
-// selects the warp-specialized varlen_prefill_ws_kernel.
-enum { kPrefillSplitWaves = 0, kPrefillRing = 1 };
-inline int prefill_impl() {
-  static const int impl = [] {
-    const char* e = getenv("NDL_PREFILL_IMPL");
-    return (e != nullptr && e[0] == 's') ? (int)kPrefillSplitWaves : (int)kPrefillRing;
-  }();
-  return impl;
-}
-
-// Launch of varlen_prefill_ws_kernel (arguments already checked by ndl_varlen_prefill).
-// Workgroup: the group's query heads in chunks of at most kWsMaxPairs, times 32-row
-// subtiles while the pairs stay within kWsMaxPairs; two waves per (head, subtile).
-static int launch_prefill_ws(void* out, const void* q, int64_t q_tok_stride,
-                             const void* kv_cache, int64_t num_blocks,
-                             const int32_t* block_table, int64_t bt_row_stride,
-                             int max_blocks_per_seq, const int32_t* cu_seqlens,
-                             const int32_t* context_lens, int num_seqs, int64_t num_tokens,
-                             int max_seqlen, int num_heads, int num_kv_heads, int head_dim,
-                             float scale, ndl_stream_t stream) {
-  const int group = num_heads / num_kv_heads;
-  const int chunks = (group + kWsMaxPairs - 1) / kWsMaxPairs;
-  const int hpw = (group + chunks - 1) / chunks;
-  int subtiles = kWsMaxPairs / hpw;
-  if (subtiles < 1) subtiles = 1;
-  const int pairs = hpw * subtiles;
-  const int waves = 2 * pairs;
-  const int wg_rows = kPrefRows * subtiles;
-  const int64_t qtiles = ((int64_t)max_seqlen + wg_rows - 1) / wg_rows;
-  const int64_t gx = (int64_t)num_kv_heads * chunks;
-  if (num_seqs > 65535 || qtiles > 65535 || gx > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
-
-  PrefillArgs a;
-  a.out = (u16*)out;
-  a.q = (const u16*)q;
-  a.q_tok_stride = q_tok_stride;
-  a.kplane = (const u16*)kv_cache;
-  a.vplane = a.kplane + num_blocks * num_kv_heads * (int64_t)16 * head_dim;
-  a.num_blocks = num_blocks;
-  a.num_kv_heads = num_kv_heads;
-  a.block_table = block_table;
-  a.bt_row_stride = bt_row_stride;
-  a.max_blocks = max_blocks_per_seq;
-  a.cu_seqlens = cu_seqlens;
-  a.context_lens = context_lens;
-  a.num_heads = num_heads;
-  a.group = group;
-  a.heads_per_wg = hpw;
-  a.head_chunks = chunks;
-  a.subtiles = subtiles;
-  a.scale_log2 = scale * kLog2e;
-  a.num_qtiles = (int)qtiles;
-  a.num_tokens = num_tokens;
-  a.num_seqs = num_seqs;
-  a.persistent = num_seqs <= kWsListSeqs && qtiles <= kWsListLevels &&
-                 gx * (int64_t)num_seqs * qtiles < ((int64_t)1 << 31);
-  const void* fn = head_dim == 128 ? (const void*)varlen_prefill_ws_kernel<128, 6>
-                                   : (const void*)varlen_prefill_ws_kernel<64, 8>;
-  dim3 grid((unsigned)gx, (unsigned)num_seqs, (unsigned)qtiles);
-  if (a.persistent) {
-    const int64_t slots = resident_workgroups(fn, 64 * waves);
-    if (slots <= 0) return NDL_ERR_LAUNCH;
-    const int64_t items = gx * (int64_t)num_seqs * qtiles;   // upper bound of the list
-    grid = dim3((unsigned)(items < slots ? items : slots), 1, 1);
-  }
-  hipStream_t s = (hipStream_t)stream;
-  if (head_dim == 128)
-    hipLaunchKernelGGL((varlen_prefill_ws_kernel<128, 6>), grid, dim3(64 * waves), 0, s, a);
-  else
-    hipLaunchKernelGGL((varlen_prefill_ws_kernel<64, 8>), grid, dim3(64 * waves), 0, s, a);
-  return check_launch();
 }
 
 }  // namespace ndl
@@ -1450,23 +882,13 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
   (void)max_context_len;
 
   const int group = num_heads / num_kv_heads;
-  if (prefill_impl() == kPrefillSplitWaves)
-    return launch_prefill_ws(out, q, q_tok_stride, kv_cache, num_blocks, block_table,
-                             bt_row_stride, max_blocks_per_seq, cu_seqlens, context_lens,
-                             num_seqs, num_tokens, max_seqlen, num_heads, num_kv_heads,
-                             head_dim, scale, stream);
 
-  // Workgroup shape: the group's query heads (in chunks of at most 8), times 32-row
-  // subtiles while that stays within 8 waves; at least kPrefLoaders waves.
-  const int chunks = (group + kPrefMaxWaves - 1) / kPrefMaxWaves;
-  const int hpw = (group + chunks - 1) / chunks;
-  int subtiles = kPrefMaxWaves / hpw;
-  if (subtiles < 1) subtiles = 1;
-  int waves = hpw * subtiles;
-  if (waves < kPrefLoaders) waves = kPrefLoaders;
-  const int wg_rows = kPrefRows * subtiles;
-  const int64_t qtiles = ((int64_t)max_seqlen + wg_rows - 1) / wg_rows;
-  const int64_t gx = (int64_t)num_kv_heads * chunks;
+  // Eight jobs (query head, 32-row subtile) per workgroup; a (sequence, kv head) pair has
+  // group * ceil(rows / 32) jobs.
+  const int waves = kPrefWaves;
+  const int64_t qtiles = (((int64_t)max_seqlen + kPrefRows - 1) / kPrefRows * group +
+                          kPrefWaves - 1) / kPrefWaves;
+  const int64_t gx = num_kv_heads;
   if (num_seqs > 65535 || qtiles > 65535 || gx > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
 
   PrefillArgs a;
@@ -1484,9 +906,6 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
   a.context_lens = context_lens;
   a.num_heads = num_heads;
   a.group = group;
-  a.heads_per_wg = hpw;
-  a.head_chunks = chunks;
-  a.subtiles = subtiles;
   a.scale_log2 = scale * kLog2e;
   a.num_qtiles = (int)qtiles;
   a.num_tokens = num_tokens;
