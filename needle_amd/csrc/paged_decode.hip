@@ -33,7 +33,7 @@
 //
 // Small batches (kv heads x sequences x NW waves within the resident waves, at most 16
 // tiles per wave): one workgroup of NW waves (16 at head_dim 64, 8 at 128) per (kv head,
-// sequence) instead.  Each wave takes 1/NW of the sequence's tiles through the same
+// sequence) instead.  Wave w takes every NW-th tile (w, w + NW, ..) through the same
 // per-tile code, and the waves
 // combine their (m, l, acc) through LDS: one launch, no workspace traffic.  With few
 // sequences the stream split would cut every sequence into many 2-tile pieces and the
@@ -165,8 +165,8 @@ __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
 }
 
 // NW == 1: one wave per workgroup, wave s of a kv head takes stream tiles s*C .. s*C + C.
-// NW > 1: one workgroup per (kv head, sequence); wave w takes tiles w*C .. w*C + C of
-// the sequence (C = ceil(n / NW)) and the waves combine through LDS.
+// NW > 1: one workgroup per (kv head, sequence); wave w takes tiles w, w + NW, .. of the
+// sequence and the waves combine through LDS.
 // Two waves per SIMD for the default two-deep stream kernel (its 256-register budget), so
 // that the fused append's few extra registers do not halve its occupancy.
 template <int D, int NBUF, int NW, bool APP, bool ROPE = false>
@@ -245,8 +245,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
 
   // Tiles lt0 .. lt1 of sequence seq (n_tiles in all) for the g heads of kv head kvh,
   // as segment segid of this kv head.
+  // The tiles are lt0, lt0 + NW, .. below lt1 (consecutive in the stream split, every
+  // NW-th in the per-sequence split); first_bt, if not null, holds this lane's block id of
+  // the first window (column lt0 + NW * lane, clamped to the row), loaded by the caller.
+  constexpr int stride = NW;
   auto segment = [&](const int seq, const int lt0, const int lt1, const int n_tiles,
-                     const int segid) {
+                     const int segid, const int* first_bt) {
     const int64_t L = attended_len(a, seq);
     const int t1 = (int)(lt1 * 16 < L ? lt1 * 16 : L);   // one past the last token attended
 
@@ -286,7 +290,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     // DPL*c .. of V.  The row is stored while the segment's first tile computes: stores
     // count in the in-order memory counter, and stored there, only loads issued after it
     // (a tile later) wait for it.
-    const bool app = APP && lt1 == n_tiles;   // wave-uniform
+    // wave-uniform: this wave attends the sequence's last tile
+    const bool app = APP && lt1 == n_tiles && (n_tiles - 1 - lt0) % stride == 0;
     const int r_new = app ? a.context_lens[seq] & 15 : 0;
     u32x4 k_app = {0u, 0u, 0u, 0u};
     VT v_app = {};
@@ -320,9 +325,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     float m = kNegInf, lsum = 0.f;
 
     // Tiles go in windows of 64 (block ids of a window held one per lane).
-    for (int w0 = lt0; w0 < lt1; w0 += 64) {
-      const int ntiles = lt1 - w0 < 64 ? lt1 - w0 : 64;
-      const int bt_lane = lane < ntiles ? bt_row[w0 + lane] : 0;
+    for (int w0 = lt0; w0 < lt1; w0 += 64 * stride) {
+      const int left = (lt1 - w0 + stride - 1) / stride;          // tiles from w0 on
+      const int ntiles = left < 64 ? left : 64;
+      const int bt_lane = (first_bt != nullptr && w0 == lt0) ? *first_bt
+                          : lane < ntiles ? bt_row[w0 + stride * lane] : 0;
 
       auto load_tile = [&](int it, Tile& t) {
         int64_t blk = __builtin_amdgcn_readlane(bt_lane, it);
@@ -337,7 +344,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       };
 
       auto compute_tile = [&](int it, Tile& t) {
-        if (kStoreRow && app && w0 + it == lt0 && app_blk >= 0) {   // the segment's first tile
+        const int tix = w0 + stride * it;   // the tile's index in the sequence
+        if (kStoreRow && app && tix == lt0 && app_blk >= 0) {   // the segment's first tile
           u16* const kb = const_cast<u16*>(a.kplane) + app_blk * blk_stride + head_off + r_new * D;
           u16* const vb = const_cast<u16*>(a.vplane) + app_blk * blk_stride + head_off + r_new * D;
           if (k_row == r_new % RPI) st16(kb + 8 * k_chunk, k_app);
@@ -348,7 +356,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
               *reinterpret_cast<VT*>(vb + DPL * c) = v_app;
           }
         }
-        if (app && w0 + it == n_tiles - 1 && !t.bad) {   // the appended token's tile
+        if (app && tix == n_tiles - 1 && !t.bad) {   // the appended token's tile
 #pragma unroll
           for (int s = 0; s < KS; ++s)
             if (RPI * s + k_row == r_new) t.k[s] = k_app;
@@ -371,9 +379,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
           st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka), qb[s], st,
                                                        0, 0, 0);
         }
-        // st[i] is the score of token (w0+it)*16 + 4j + i for head c.
-        const int pos0 = (w0 + it) * 16 + 4 * j;
-        const bool partial = t.bad || ((w0 + it) * 16 + 16 > t1);  // wave-uniform
+        // st[i] is the score of token tix*16 + 4j + i for head c.
+        const int pos0 = tix * 16 + 4 * j;
+        const bool partial = t.bad || (tix * 16 + 16 > t1);  // wave-uniform
         float sc[4];
         float mt = kNegInf;
 #pragma unroll
@@ -498,18 +506,21 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       if (nt > 0) {
         const int64_t s0 = start > first ? start : first;
         const int64_t s1 = end < first + nt ? end : first + nt;
-        segment(seq, (int)(s0 - first), (int)(s1 - first), nt, sw + seq);
+        segment(seq, (int)(s0 - first), (int)(s1 - first), nt, sw + seq, nullptr);
       }
       first += nt;
       ++seq;
     }
     if (held_seg >= 0) store_partial(held_seg, held, held_m, held_l);
   } else {
+    // Wave w takes tiles w, w + NW, w + 2 NW, .. of the sequence.  Their block ids (one
+    // column per lane) do not depend on the context length, so they load alongside it.
     const int seq = sw;
+    const int col = wv + NW * lane;
+    const int first_bt =
+        a.block_table[(int64_t)seq * a.bt_row_stride + (col < a.max_blocks ? col : a.max_blocks - 1)];
     const int nt = seq_tiles(a, seq);
-    const int per = (nt + NW - 1) / NW;
-    const int lt0 = wv * per, lt1 = lt0 + per < nt ? lt0 + per : nt;
-    if (lt0 < lt1) segment(seq, lt0, lt1, nt, 0);
+    if (wv < nt) segment(seq, wv, nt, nt, 0, &first_bt);
     // Combine: every wave's (m, l) and accumulators to LDS (the K tiles are dead once
     // all waves are past their loop), then wave w finishes elements w*KPW .. + KPW of
     // every lane over the NW waves in a fixed order.  A sequence with nothing to attend
