@@ -488,11 +488,41 @@ def long_context_decode(torch, ops, wl, reps, cpu=True):
     return res
 
 
+def llama_tp8_share(torch, ops, wl, reps):
+    """One GPU's share of the Llama-3-8B decode under 8-way tensor parallelism (kv heads
+    split across GPUs): 4 query heads over 1 kv head, the configuration's 64 sequences and
+    context lengths, 32 layer pools, the fused append + attention launch replayed from a
+    graph.  A sharding illustration, not one of the configurations (no CPU baseline)."""
+    dev = torch.device("cuda:0")
+    shape = wl.HeadShape(4, 1, 128)
+    ctx = wl.llama8b_decode_ctx()
+    cases = [wl.decode_case(shape, ctx, seed=1002 + l, device=dev, garbage=False)
+             for l in range(LAYERS)]
+
+    def step():
+        for c in cases:
+            ops.paged_decode(c.q, c.kv_cache, c.block_table, c.context_lens, shape.scale,
+                             shape.num_heads, shape.num_kv_heads, shape.head_dim,
+                             new_k=c.k, new_v=c.v)
+    step()
+    g = capture(torch, step)
+    ms = time_region(torch, g.replay, reps) / LAYERS
+    del g
+    b = wl.decode_bytes(shape, ctx, cases[0].block_table.shape[1]) + \
+        wl.append_bytes(shape, len(ctx), len(ctx), varlen=False)
+    return {"us_per_layer": round(ms * 1e3, 2), "gbs": round(b / ms / 1e6, 1),
+            "frac_of_hbm_peak": round(b / ms / 1e6 / HBM_PEAK_GBS, 4),
+            "algorithmic_bytes": b, "heads": "4 q / 1 kv per GPU (tp 8)",
+            "note": "one GPU's share at 8-way tensor parallelism; the all-reduce after o_proj "
+                    "and every other collective are not part of it"}
+
+
 def extra_measurements(torch, ops, wl, reps, cpu_budget, cpu=True):
     """The other shapes, each with its CPU baseline (the reference torch path restated)."""
     return {"qwen2_0.5b_decode": qwen05b_decode(torch, ops, wl, reps, cpu_budget, cpu=cpu),
             "qwen2_7b_prefill": qwen7b_prefill(torch, ops, wl, reps, cpu=cpu),
-            "llama3_8b_long_context_decode": long_context_decode(torch, ops, wl, reps, cpu=cpu)}
+            "llama3_8b_long_context_decode": long_context_decode(torch, ops, wl, reps, cpu=cpu),
+            "llama3_8b_decode_tp8_share": llama_tp8_share(torch, ops, wl, reps)}
 
 
 def ceilings(torch):

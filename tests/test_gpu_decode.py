@@ -282,3 +282,21 @@ def test_batch_sizes_around_one_wave_of_sequences(nseq, part):
                                     case.context_lens[live], s.scale, s.num_heads,
                                     s.num_kv_heads, s.head_dim)
     assert_close(got[live], want.float())
+
+
+@pytest.mark.parametrize("part", [0, -1])
+def test_llama_decode_tp8_share(part):
+    # One GPU's share of the Llama-3-8B decode under 8-way tensor parallelism (kv heads split
+    # across GPUs, attention.py:45-46): 4 query heads over 1 kv head, the configuration's 64
+    # sequences and context lengths, fused append.
+    shape = wl.HeadShape(4, 1, 128)
+    case = wl.decode_case(shape, wl.llama8b_decode_ctx(), seed=1002)
+    g = case.to(DEV)
+    s = case.shape
+    got = ops.paged_decode(g.q, g.kv_cache, g.block_table, g.context_lens, s.scale,
+                           s.num_heads, s.num_kv_heads, s.head_dim, partition_tokens=part,
+                           new_k=g.k, new_v=g.v)
+    torch.cuda.synchronize()
+    want, pool = run_oracle(case)
+    assert torch.equal(g.kv_cache.cpu().view(torch.int16), pool.view(torch.int16))
+    assert_close(got.float().cpu(), want)
