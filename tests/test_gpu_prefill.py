@@ -74,10 +74,14 @@ def test_qwen2_7b_prefill_sampled_rows_vs_fp64():
         assert_close(got[sub], want)
 
 
+# Group sizes 1..9 and 16: a workgroup's eight (head, 32-row subtile) jobs span one subtile
+# (g = 8, 16), two (g = 4 .. 7, 9) or more (g = 1, 2, 3), with subtile boundaries at every
+# offset inside the eight.
 @pytest.mark.parametrize("shape", [
     wl.QWEN2_7B, wl.LLAMA3_8B, wl.QWEN2_05B, wl.HeadShape(8, 8, 128), wl.HeadShape(16, 2, 128),
     wl.HeadShape(8, 1, 64), wl.HeadShape(12, 4, 64), wl.HeadShape(16, 1, 128),
-    wl.HeadShape(18, 2, 64)])
+    wl.HeadShape(18, 2, 64), wl.HeadShape(4, 2, 128), wl.HeadShape(10, 2, 128),
+    wl.HeadShape(12, 2, 64)])
 def test_shapes_and_edge_lengths(shape):
     lens = [1, 15, 16, 17, 31, 32, 33, 127, 128, 129, 300]
     case = wl.prefill_case(shape, lens, seed=301)
