@@ -17,8 +17,9 @@
 //     wave masks past its own rows.
 //   * K/V advance 32 keys (two cache blocks) per step through an NS-stage LDS ring
 //     filled by direct global->LDS loads (global_load_lds_dwordx4, no register
-//     staging); each instruction reads whole rows, 1 KiB contiguous, and lands
-//     them with a row-dependent 16-byte chunk swizzle.
+//     staging), 1 KiB per instruction: a K piece is whole rows (contiguous), landed
+//     with a row-dependent 16-byte chunk swizzle; a V piece is 64 bytes of each of a
+//     block's 16 rows.
 //   * S^T = K Q^T on v_mfma_f32_32x32x16_bf16: A = K rows from LDS
 //     (ds_read_b128), B = Q^T held in registers.  Lane l holds the scores of query
 //     row l%32 for 16 of the 32 keys, so a row max needs one permlane32 swap.
