@@ -627,7 +627,55 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
         for (int e = 0; e < IPW; ++e)
           lds_dma16(base, ld_off[e], lds + 1024 * e);
       };
+      // Byte offset of a block in a plane: Hkv * 16 * D * 2 bytes per block fits 32 bits.
+      const uint32_t blk_bytes = (uint32_t)(blk_stride * 2);
       while (step < lim && badbits == 0) {
+        // Fast trips: every per-trip check of the trip below holds for the whole run, so it
+        // is tested once: both steps staged (step + NS - 2, step + NS - 1) exist and their
+        // four table columns lie inside the current window and the table row (no clamp);
+        // the window has no invalid id (badbits stays 0); step + 2 is a full step (no V
+        // rows to clear); the ring is in full flow (a constant load wait).  What is left
+        // per trip is the barrier, two block look-ups and their loads.
+        if (!win_bad) {
+          const int wcols = win0 + 64 < a.max_blocks ? win0 + 64 : a.max_blocks;
+          int end = lim;
+          if (nsteps - NS + 1 < end) end = nsteps - NS + 1;            // step + NS - 1 exists
+          if (kv_end / kPrefKeys - 2 < end) end = kv_end / kPrefKeys - 2;   // step + 2 full
+          if ((wcols - 2 * NS + 2) / 2 < end) end = (wcols - 2 * NS + 2) / 2;  // columns
+          for (; step < end; step += 2) {
+            const int stage1 = stage + 1 == NS ? 0 : stage + 1;
+            const int stage2 = stage1 + 1 == NS ? 0 : stage1 + 1;
+            vm_wait<(NS - 5) * IPW>();
+            lds_barrier();
+            u32x4 ka[KS];
+            bf16x8 vop[2 * DT];
+            k_reads(stage1, ka);
+            v_reads(stage, vop);
+            st1 = qk(ka);
+            {
+              // This wave's block of steps step + NS - 2 and step + NS - 1: table columns
+              // ci and ci + 2 of the window.
+              const int ci = 2 * (step + NS - 2) + ld_blk - win0;
+              const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane(btw, ci);
+              const uint32_t b1 = (uint32_t)__builtin_amdgcn_readlane(btw, ci + 2);
+              const u16* base0 = (const u16*)((const char*)ld_head + (uint64_t)b0 * blk_bytes);
+              const u16* base1 = (const u16*)((const char*)ld_head + (uint64_t)b1 * blk_bytes);
+              const uint32_t l0 = ld_lds + (uint32_t)slot_after(stage, NS - 2) * (kPrefKeys * D * 2);
+              const uint32_t l1 = ld_lds + (uint32_t)slot_after(stage, NS - 1) * (kPrefKeys * D * 2);
+#pragma unroll
+              for (int e = 0; e < IPW; ++e) lds_dma16(base0, ld_off[e], l0 + 1024 * e);
+#pragma unroll
+              for (int e = 0; e < IPW; ++e) lds_dma16(base1, ld_off[e], l1 + 1024 * e);
+            }
+            finish(step, stage, st0, vop, false);
+            k_reads(stage2, ka);
+            v_reads(stage1, vop);
+            st0 = qk(ka);
+            finish(step + 1, stage1, st1, vop, false);
+            stage = stage2;
+          }
+          if (step >= lim) break;
+        }
         const int stage1 = stage + 1 == NS ? 0 : stage + 1;
         const int stage2 = stage1 + 1 == NS ? 0 : stage1 + 1;
         // Loads of steps up to step + 2 (the last one at most) landed: steps issued after
