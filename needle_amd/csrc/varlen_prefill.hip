@@ -189,9 +189,18 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
   __shared__ __attribute__((aligned(16))) u16 lk[NS][kPrefKeys * D];
   __shared__ __attribute__((aligned(16))) u16 lv[NS][kPrefKeys * D];
   __shared__ uint32_t lds_sink[64];   // destination of the L2 warm-up loads, never read
+  __shared__ int32_t s_btw[64];       // first table window of the tile (prefetched)
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // provably wave-uniform
+  // The lane number through an empty asm: per-lane offsets computed from it stay where they
+  // are used instead of being hoisted out of the tile loop (and kept live, in registers
+  // the ring needs, or spilled).
+  auto fresh_lane = [&] {
+    int l = lane;
+    asm volatile("" : "+v"(l));
+    return l;
+  };
   const int r32 = lane & 31, h = lane >> 5;
 
   // The look-up reads through the scalar cache (constant address space; the kernel never
@@ -220,7 +229,10 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
   // workgroup barriers).  ahead() resolves nx, the tile this workgroup takes next
   // (n == 0: none); it runs while the tile's first loads are in flight, and nx's Q rows
   // and table window are pulled into the L2 at the end of this tile.
+  bool btw_next = false;
   auto tile = [&](const PrefTile& t, const PrefTile& nx, auto&& ahead) {
+    const bool pre = btw_next;
+    btw_next = false;
     int64_t tok0;
     int n, ctx;
     if (!bounds(t, tok0, n, ctx)) {
@@ -253,27 +265,18 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     // and one wait covers both; a later refill waits for every outstanding load (a
     // vector-memory wait cannot single one out); it happens once per 64 blocks.
     int win0 = 0;
-    int btw = lane < a.max_blocks ? bt_row[lane] : 0;
-
-    // B operand of S^T = K Q^T: lane l supplies Q[row l%32][16 s + 8 h .. + 8).
-    bf16x8 qb[KS];
-    {
-      // Unconditional loads (rows past the range read the tile's first row and are
-      // zeroed), so that no branch hides them from the compiler's load counting.
-      const int row = wrow0 + r32;
-      const bool ok = wave_active && row < n;
-      const u16* qrow = a.q + (tok0 + (ok ? row : 0)) * a.q_tok_stride + (int64_t)head * D + 8 * h;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const u32x4 w = ld16(qrow + 16 * s);
-        qb[s] = __builtin_bit_cast(bf16x8, ok ? w : u32x4{0u, 0u, 0u, 0u});
-      }
+    int btw = 0;
+    if (!pre && wave == 0) {
+      const int l = fresh_lane();
+      lds_dma4(bt_row, 4u * (uint32_t)(l < a.max_blocks ? l : a.max_blocks - 1), lds_addr(s_btw));
+      vm_wait<0>();
     }
-    // The Q loads stay in flight while the ring's first steps are issued: vector-memory
-    // loads complete in issue order, so the ring's wait for step 0 covers them (and the
-    // table window, and the previous tile's L2 warm-up loads).  Loads issued after a
-    // step's (window refills) only make a ring wait, which counts the direct loads
-    // issued after that step, wait longer, never shorter.
+
+    // B operand of S^T = K Q^T: lane l supplies Q[row l%32][16 s + 8 h .. + 8), read from
+    // LDS at the ring start (below).  Loads issued after a step's (window refills) only
+    // make a ring wait, which counts the direct loads issued after that step, wait longer,
+    // never shorter: vector-memory loads complete in issue order.
+    bf16x8 qb[KS];
 
     // Every wave stages, per step, IPW of the PIECES / 2 pieces (1 KiB, one direct load
     // each) that block ld_blk of the step holds in plane ld_plane (K, V): pieces
@@ -312,12 +315,13 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     // direct loads of it.  An invalid block id reads block 0 instead (always mapped);
     // rows past the range read whatever the table maps them to.  The softmax masks both.
     // A window of the table with no invalid id (the normal case) sets no bits.
-    bool win_bad = __builtin_amdgcn_ballot_w64(lane < a.max_blocks && (uint32_t)btw >= nb32) != 0;
+    bool win_bad = false;
     auto stage_in = [&](int step, int stage) {
       const int c0 = clamp_col(2 * step), c1 = clamp_col(2 * step + 1);  // same 64-window
       if (c0 < win0 || c0 >= win0 + 64) {
         win0 = c0 & ~63;
-        btw = win0 + lane < a.max_blocks ? bt_row[win0 + lane] : 0;
+        const int l = fresh_lane();
+        btw = win0 + l < a.max_blocks ? bt_row[win0 + l] : 0;
         vm_wait<0>();
         win_bad = __builtin_amdgcn_ballot_w64(win0 + lane < a.max_blocks &&
                                               (uint32_t)btw >= nb32) != 0;
@@ -586,15 +590,61 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       finish(step, stage, st_cur, vop, true);
     };
 
-    // Ring: steps 0 .. NS-3 in flight at the start.  The first barrier retires every
-    // wave's reads of the previous tile (persistent launch) before the slots are refilled.
+    // Ring start: steps 0 .. NS-3 in flight before the first trip.  The first barrier
+    // retires every wave's reads of the previous tile (persistent launch) before the slots
+    // are refilled.  Steps 0 and 1 go out first.  The wave's Q rows are staged in one plane
+    // of slots 2 .. 5, free until step 2 is staged (wave w: the K plane of slot 2 + w/2 for
+    // even w, else its V plane), by whole-row direct loads (RPP rows per instruction, the K
+    // pieces' row-dependent chunk swizzle), and read back in the operand layout: loading
+    // the operand layout from memory directly (32 rows x 32 bytes per instruction) moves a
+    // third of the bytes per cycle that whole rows do through the CU's memory path.  Rows
+    // past the range load the wave's first row (the tile's first row for a wave with no
+    // rows) and are zeroed when read.  The second barrier publishes steps 0 and 1 and
+    // retires the Q reads; then steps 2 .. NS - 3 go out.
+    static_assert(NS >= 2 + kPrefWaves / 2, "Q staging planes in slots 2 ..");
     lds_barrier();
+    {
+      const int l = fresh_lane();
+      btw = l < a.max_blocks ? s_btw[l] : 0;
+      win_bad = __builtin_amdgcn_ballot_w64(l < a.max_blocks && (uint32_t)btw >= nb32) != 0;
+    }
+    stage_in(0, 0);
+    if (nsteps > 1) stage_in(1, 1);
+    u16* const qplane = (wave & 1) ? lv[2 + (wave >> 1)] : lk[2 + (wave >> 1)];
+    {
+      const u16* qbase = a.q + (tok0 + (wave_active ? wrow0 : 0)) * a.q_tok_stride +
+                         (int64_t)head * D;
+      const uint32_t ql = lds_addr(qplane);
 #pragma unroll
-    for (int t = 0; t < NS - 2; ++t)
-      if (t < nsteps) stage_in(t, t);
+      for (int e = 0; e < KS; ++e) {          // 32 rows x D x 2 bytes = KS pieces of 1 KiB
+        const int r = e * RPP + lane / CPR;
+        const int rr = wave_active && wrow0 + r < n ? r : 0;
+        const int c = (lane % CPR) ^ pref_swz<D>(r);
+        lds_dma16(qbase, (uint32_t)((rr * a.q_tok_stride + 8 * c) * 2), ql + 1024 * e);
+      }
+    }
     ahead();
-    wait_loads(nsteps - 1 < NS - 3 ? nsteps - 1 : NS - 3);
+    vm_wait<0>();   // this wave's Q rows, and steps 0 and 1, landed
+    {
+      const bool ok = wave_active && wrow0 + r32 < n;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(&qplane[koff[s]]);
+        qb[s] = __builtin_bit_cast(bf16x8, ok ? w : u32x4{0u, 0u, 0u, 0u});
+      }
+    }
     lds_barrier();
+    if (nx.seq >= 0) {
+      if (wave == 0) {
+        const int l = fresh_lane();
+        lds_dma4(a.block_table + (int64_t)nx.seq * a.bt_row_stride,
+                 4u * (uint32_t)(l < a.max_blocks ? l : a.max_blocks - 1), lds_addr(s_btw));
+      }
+      btw_next = true;
+    }
+#pragma unroll
+    for (int t = 2; t < NS - 2; ++t)
+      if (t < nsteps) stage_in(t, t);
     if (needs_vzero(0, 0)) zero_v(0, 0);
     f32x16 st0, st1;
     {
@@ -718,6 +768,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     // L2, after the ring's last wait: direct loads into a scratch LDS word per lane that
     // nothing reads, retired by the next tile's first wait.  Lane l touches row l / 2,
     // 128-byte half l % 2 of the row's head slice.
+    if (btw_next && wave == 0) vm_wait<0>();
     int64_t ntok0;
     int nn, nctx;
     if (bounds(nx, ntok0, nn, nctx)) {
@@ -725,15 +776,13 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       const int nsub = njob / a.group, nhg = njob - nsub * a.group;
       const int nrow0 = nsub * kPrefRows;
       if (nrow0 < nn) {
-        const int r = nrow0 + (lane >> 1) < nn ? lane >> 1 : 0;
+        const int l = fresh_lane();
+        const int r = nrow0 + (l >> 1) < nn ? l >> 1 : 0;
         const u16* base = a.q + (ntok0 + nrow0) * a.q_tok_stride +
                           (int64_t)(nx.kvh * a.group + nhg) * D;
-        lds_dma4(base, (uint32_t)(r * a.q_tok_stride * 2) + (D >= 128 ? (lane & 1) * 128u : 0u),
+        lds_dma4(base, (uint32_t)(r * a.q_tok_stride * 2) + (D >= 128 ? (l & 1) * 128u : 0u),
                  lds_addr(lds_sink));
       }
-      if (wave == 0)
-        lds_dma4(a.block_table + (int64_t)nx.seq * a.bt_row_stride,
-                 4u * (uint32_t)(lane < a.max_blocks ? lane : a.max_blocks - 1), lds_addr(lds_sink));
     }
 
     if (!wave_active) return;
@@ -872,7 +921,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       const int c = i - rank * KVC;
       int seq = -1;
       for (int base = 0; base < S && seq < 0; base += 64) {
-        const int q = base + lane;
+        const int q = base + fresh_lane();
         const bool has = q < S && s_ntiles[q] > lvl;
         const uint64_t m = __builtin_amdgcn_ballot_w64(has);
         const int pc = __builtin_popcountll(m);
