@@ -254,6 +254,8 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     const bool wave_active = wrow0 < n;
     const int qpos_min = ctx + wrow0;
     const int qpos = ctx + wrow0 + r32;                          // this lane's query position
+    // Position of this wave's last query row (-1: the wave has no rows).
+    const int qpos_last = wave_active ? ctx + (wrow0 + kPrefRows <= n ? wrow0 + kPrefRows : n) - 1 : -1;
 
     const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
     const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
@@ -588,13 +590,23 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       // the row max, the growth check and the exponentials of this step run.  The upkeep
       // writes only slots no wave reads before the next barrier: those of steps before
       // this one, and V of step `need`, read after it.
+      // A step wholly past this wave's last query row (the last step of a tile whose
+      // jobs span two subtiles, for the earlier subtile's waves; every step of a wave with
+      // no rows) contributes nothing: its LDS reads, MFMAs and softmax are skipped (a
+      // wave-uniform branch; the barriers and the loads stay).  QK of step + 1 is skipped
+      // exactly when step + 1 will be.
+      // (The V reads may follow the upkeep: it writes no slot of this step.)
       u32x4 ka[KS];
       bf16x8 vop[2 * DT];
-      k_reads(nstage, ka);
-      v_reads(stage, vop);
-      st_next = qk(ka);
+      if ((step + 1) * kPrefKeys <= qpos_last) {
+        k_reads(nstage, ka);
+        st_next = qk(ka);
+      }
       if (mode != kNone) upkeep(step, stage, need, mode);
-      finish(step, stage, st_cur, vop, true);
+      if (step * kPrefKeys <= qpos_last) {
+        v_reads(stage, vop);
+        finish(step, stage, st_cur, vop, true);
+      }
     };
 
     // Ring start: steps 0 .. NS-3 in flight before the first trip.  The first barrier
