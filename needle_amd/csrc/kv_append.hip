@@ -25,12 +25,25 @@ __device__ __forceinline__ int seq_of_token(const int32_t* __restrict__ cu, int 
 // Tokens per wave at most (all of a wave's loads are issued before its slot lookups and
 // its stores).
 constexpr int kAppendMaxTokensPerWave = 4;
+// Packed batches of at most this many sequences find their tokens' sequences with one
+// vector load of cu_seqlens (lane l: boundary l) and a ballot.
+constexpr int kAppendSmallSeqs = 63;
 
-// One wave per group of tokens_per_wave consecutive tokens.  The lanes copy a token's
+// One wave per group of TPW consecutive tokens.  The lanes copy a token's
 // num_kv_heads * head_dim / 8 16-byte chunks of both planes (one 1 KiB instruction per
-// plane when num_kv_heads * head_dim = 512).  The slot of a token is wave-uniform
-// (sequence by binary search over cu_seqlens, position, table column, block), so those
-// lookups go through the scalar cache once per token.
+// plane when num_kv_heads * head_dim = 512).  The slot of a token is wave-uniform.
+//   SMALL (cu_seqlens given, num_seqs <= kAppendSmallSeqs): lane l loads cu_seqlens[l] and
+//     context_lens[l] with two vector loads issued before the rows, so they return first
+//     (vector loads complete in issue order); a token's sequence is the number of
+//     boundaries at or below it, less one (a ballot: the largest i with cu[i] <= t, empty
+//     sequences included), its context length a readlane; only the table entries are
+//     scalar loads, one per token, all in flight together.
+//   otherwise: sequence by binary search over cu_seqlens (scalar loads, their own counter,
+//     in flight while the rows load), or the token itself without cu_seqlens (decode).
+// TPW is a template argument so that every wave issues the same loads and the compiler's
+// vector-memory waits count them exactly; the last wave reloads its last valid token's
+// row for the tokens past the end and stores nothing for them.
+template <int TPW, bool SMALL>
 __global__ __launch_bounds__(256) void kv_append_kernel(
     u16* __restrict__ cache, int64_t plane_elems, int64_t num_blocks, int num_kv_heads,
     int block_size, int head_dim,
@@ -38,26 +51,43 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     const u16* __restrict__ v, int64_t v_tok_stride,
     const int32_t* __restrict__ block_table, int64_t bt_row_stride, int max_blocks,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ context_lens,
-    int num_seqs, int64_t num_tokens, int tokens_per_wave) {
+    int num_seqs, int64_t num_tokens) {
   const int lane = threadIdx.x & 63;
   const int64_t wave_id =
       (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
-  const int64_t t0 = wave_id * tokens_per_wave;
+  const int64_t t0 = wave_id * TPW;
   const int cpr = head_dim >> 3;         // chunks per (token, kv head) row
   const int cpt = num_kv_heads * cpr;    // chunks per token and plane
-  const int64_t packed = cu_seqlens == nullptr ? num_tokens : (int64_t)cu_seqlens[num_seqs];
+
+  // SMALL: lane l's boundary cu_seqlens[l] (l <= num_seqs) and context length.
+  int cu_l = 0, ctx_l = 0;
+  if constexpr (SMALL) {
+    cu_l = cu_seqlens[lane <= num_seqs ? lane : num_seqs];
+    ctx_l = context_lens[lane < num_seqs ? lane : num_seqs - 1];
+  }
 
   // Destination row (element offset in a plane) of each token, or -1 when it is skipped.
-  int64_t dst_row[kAppendMaxTokensPerWave];
+  int64_t dst_row[TPW];
   auto lookup = [&]() {
+    int64_t packed;
+    if constexpr (SMALL)
+      packed = __builtin_amdgcn_readlane(cu_l, num_seqs);
+    else
+      packed = cu_seqlens == nullptr ? num_tokens : (int64_t)cu_seqlens[num_seqs];
 #pragma unroll
-    for (int u = 0; u < kAppendMaxTokensPerWave; ++u) {
+    for (int u = 0; u < TPW; ++u) {
       dst_row[u] = -1;
       const int64_t t = t0 + u;
-      if (u >= tokens_per_wave || t >= num_tokens || t >= packed) continue;
+      if (t >= num_tokens || t >= packed) continue;
       int i;
       int64_t p;
-      if (cu_seqlens == nullptr) {
+      if constexpr (SMALL) {
+        const uint64_t m = __builtin_amdgcn_ballot_w64(lane <= num_seqs && (int64_t)cu_l <= t);
+        i = __builtin_popcountll(m) - 1;
+        if (i < 0 || i >= num_seqs) continue;   // only for a malformed cu_seqlens
+        p = (int64_t)__builtin_amdgcn_readlane(ctx_l, i) +
+            (t - __builtin_amdgcn_readlane(cu_l, i));
+      } else if (cu_seqlens == nullptr) {
         i = (int)t;
         p = context_lens[i];
       } else {
@@ -76,24 +106,24 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
   // slot lookups while the loads are in flight (the source rows depend only on the
   // token), then the stores.  Lanes past the row's chunks load its last chunk again (no
   // divergent branch around the loads, so they go out back to back) and store nothing.
+  const int64_t t_last = num_tokens - 1;
   auto round = [&](const int r, const bool first) {
     const int cc0 = r * 64 + lane;
     const bool live = cc0 < cpt;
     const int cc = live ? cc0 : cpt - 1;
     const int h = cc / cpr, c = cc - h * cpr;
     const int64_t in_off = (int64_t)h * head_dim + c * 8;
-    u32x4 kr[kAppendMaxTokensPerWave], vr[kAppendMaxTokensPerWave];
+    u32x4 kr[TPW], vr[TPW];
 #pragma unroll
-    for (int u = 0; u < kAppendMaxTokensPerWave; ++u) {
-      if (u < tokens_per_wave && t0 + u < num_tokens) {  // wave-uniform
-        kr[u] = ld16(k + (t0 + u) * k_tok_stride + in_off);
-        vr[u] = ld16(v + (t0 + u) * v_tok_stride + in_off);
-      }
+    for (int u = 0; u < TPW; ++u) {
+      const int64_t t = t0 + u < num_tokens ? t0 + u : t_last;
+      kr[u] = ld16(k + t * k_tok_stride + in_off);
+      vr[u] = ld16(v + t * v_tok_stride + in_off);
     }
     if (first) lookup();
     const int64_t out_off = ((int64_t)h * block_size) * head_dim + c * 8;
 #pragma unroll
-    for (int u = 0; u < kAppendMaxTokensPerWave; ++u) {
+    for (int u = 0; u < TPW; ++u) {
       if (live && dst_row[u] >= 0) {
         st16(cache + dst_row[u] + out_off, kr[u]);
         st16(cache + plane_elems + dst_row[u] + out_off, vr[u]);
@@ -132,10 +162,11 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
   if ((k_tok_stride | v_tok_stride) & 7) return NDL_ERR_INVALID_ARG;
 
   const int64_t plane_elems = num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
+  const bool small = cu_seqlens != nullptr && num_seqs <= kAppendSmallSeqs;
   // As few tokens per wave as keep every wave resident at once (a second, partial round
   // of waves costs more than longer waves: 17,705 tokens of 4 x 128 went 13.3 us at 1
   // or 2 tokens per wave, 12.9 us at 3, 14.1 us at 4 on MI355X).
-  int64_t resident = resident_workgroups((const void*)kv_append_kernel, 256) * 4;
+  int64_t resident = resident_workgroups((const void*)kv_append_kernel<1, false>, 256) * 4;
   if (resident <= 0) resident = 8192;
   int64_t tpw64 = (num_tokens + resident - 1) / resident;
   const int tpw = (int)(tpw64 < 1 ? 1 : tpw64 > kAppendMaxTokensPerWave ? kAppendMaxTokensPerWave
@@ -143,10 +174,20 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
   const int64_t waves = (num_tokens + tpw - 1) / tpw;
   const int64_t blocks = (waves + 3) / 4;
   if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
-  hipLaunchKernelGGL(kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0,
-                     (hipStream_t)stream, (u16*)kv_cache, plane_elems, num_blocks, num_kv_heads,
-                     block_size, head_dim, (const u16*)k, k_tok_stride, (const u16*)v,
-                     v_tok_stride, block_table, bt_row_stride, max_blocks_per_seq, cu_seqlens,
-                     context_lens, num_seqs, num_tokens, tpw);
+  const void* fns[2][kAppendMaxTokensPerWave] = {
+      {(const void*)kv_append_kernel<1, false>, (const void*)kv_append_kernel<2, false>,
+       (const void*)kv_append_kernel<3, false>, (const void*)kv_append_kernel<4, false>},
+      {(const void*)kv_append_kernel<1, true>, (const void*)kv_append_kernel<2, true>,
+       (const void*)kv_append_kernel<3, true>, (const void*)kv_append_kernel<4, true>}};
+  u16* cache = (u16*)kv_cache;
+  const u16* kp = (const u16*)k;
+  const u16* vp = (const u16*)v;
+  void* args[] = {&cache, (void*)&plane_elems, &num_blocks, &num_kv_heads, &block_size,
+                  &head_dim, &kp, &k_tok_stride, &vp, &v_tok_stride, &block_table,
+                  &bt_row_stride, &max_blocks_per_seq, &cu_seqlens, &context_lens, &num_seqs,
+                  &num_tokens};
+  if (hipLaunchKernel(fns[small ? 1 : 0][tpw - 1], dim3((unsigned)blocks), dim3(256), args, 0,
+                      (hipStream_t)stream) != hipSuccess)
+    return NDL_ERR_LAUNCH;
   return check_launch();
 }
