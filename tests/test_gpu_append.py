@@ -3,6 +3,7 @@
 The pool is pre-filled with random bit patterns outside the owned slots, so a
 stray write anywhere shows up in the byte compare.
 """
+import numpy as np
 import pytest
 import torch
 
@@ -123,3 +124,16 @@ def test_varlen_append_many_tokens_odd_rows_and_skips():
     ops.write_kv(kg, vg, g.kv_cache, bt.to(DEV), g.cu_seqlens, g.context_lens)
     torch.cuda.synchronize()
     assert torch.equal(_bits(g.kv_cache.cpu()), _bits(want))
+
+
+@pytest.mark.parametrize("num_seqs", [63, 64, 150])
+def test_varlen_append_batch_sizes_around_the_ballot_lookup(num_seqs):
+    """Up to 63 packed sequences find their tokens' sequences with one vector load of
+    cu_seqlens and a ballot; 64 and more take the binary search.  Empty prompts and cached
+    prefixes sit at the ends and in the middle of the batch."""
+    rng = np.random.default_rng(110 + num_seqs)
+    lens = rng.integers(0, 40, size=num_seqs)
+    lens[[0, num_seqs // 2, num_seqs - 1]] = [0, 0, 0]
+    ctx = rng.integers(0, 50, size=num_seqs)
+    case = wl.prefill_case(wl.QWEN2_7B, lens.tolist(), seed=110 + num_seqs, ctx_lens=ctx.tolist())
+    _varlen_parity(case)
