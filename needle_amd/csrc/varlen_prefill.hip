@@ -522,14 +522,17 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       const bool masked = kv0 + kPrefKeys - 1 > qpos_min || kv0 + kPrefKeys > kv_end ||
                           ((badbits >> (2 * stage)) & 3u) != 0;
       if (may_mask && masked) {
-        const bool bad0 = (badbits >> (2 * stage)) & 1u;
-        const bool bad1 = (badbits >> (2 * stage + 1)) & 1u;
+        // Element r holds key kv0 + 4h + o(r), o(r) = 8 (r/4) + r%4 (o < 16 exactly for
+        // r < 8, the step's first block).  It is attended iff key <= qpos, key < kv_end and
+        // its block is valid, i.e. o(r) <= one limit per lane and block: one compare each.
+        const int base = kv0 + 4 * h;
+        const int lim = min(qpos, kv_end - 1) - base;
+        const int lim0 = (badbits >> (2 * stage)) & 1u ? -1 : lim;
+        const int lim1 = (badbits >> (2 * stage + 1)) & 1u ? -1 : lim;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int key = 8 * (r >> 2) + 4 * h + (r & 3);
-          const int kp = kv0 + key;
-          const bool ok = kp <= qpos && kp < kv_end && !(key < 16 ? bad0 : bad1);
-          st[r] = ok ? st[r] : kNegInf;
+          const int o = 8 * (r >> 2) + (r & 3);
+          st[r] = o <= (r < 8 ? lim0 : lim1) ? st[r] : kNegInf;
         }
       }
       // Exponentials against the running max as it stands.  A row whose max grew by
