@@ -554,23 +554,29 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
         mx = half_max(mx);
         const float m_new = fmaxf(m_run, mx * a.scale_log2);
         if (m_new != m_run) {
-          // The accumulator is scaled in place (tied asm operands: a plain multiply lets
-          // the register allocator give the scaled accumulator new registers and copy it
-          // back on every step).  0 when m_run is -inf (nothing accumulated yet).
-          const float alpha = fast_exp2(m_run - m_new);
-          // The compiler's hazard tracking does not look into inline asm: the first
-          // multiply carries the wait state a VALU read of a transcendental's result
-          // needs (without it, it reads the register's previous contents).
+          // While m_run is -inf every probability so far was 0 (V rows that could hold
+          // non-finite bits are cleared), so the accumulator and the sum are 0 and need no
+          // rescale: a row's first attended step (every wave's first step of a tile)
+          // skips it.
+          if (m_run != kNegInf) {
+            // The accumulator is scaled in place (tied asm operands: a plain multiply lets
+            // the register allocator give the scaled accumulator new registers and copy it
+            // back on every step).
+            const float alpha = fast_exp2(m_run - m_new);
+            // The compiler's hazard tracking does not look into inline asm: the first
+            // multiply carries the wait state a VALU read of a transcendental's result
+            // needs (without it, it reads the register's previous contents).
 #pragma unroll
-          for (int t = 0; t < DT; ++t)
+            for (int t = 0; t < DT; ++t)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              if (t == 0 && i == 0)
-                asm volatile("s_nop 1\n\tv_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
-              else
-                asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
-            }
-          l_run *= alpha;
+              for (int i = 0; i < 16; ++i) {
+                if (t == 0 && i == 0)
+                  asm volatile("s_nop 1\n\tv_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
+                else
+                  asm volatile("v_mul_f32 %0, %0, %1" : "+v"(acc[t][i]) : "v"(alpha));
+              }
+            l_run *= alpha;
+          }
           m_run = m_new;
         }
         lstep = 0.f;
