@@ -387,23 +387,6 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
                                                      0, 0, 0);
       return st;
     };
-    // The same product with the K operands read in two halves (fewer live registers).
-    auto qk_halves = [&](int stage) {
-      const u16* kt = lk[stage];
-      f32x16 st = {};
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        u32x4 ka[KS / 2];
-#pragma unroll
-        for (int s = 0; s < KS / 2; ++s)
-          ka[s] = *reinterpret_cast<const u32x4*>(&kt[koff[half * KS / 2 + s]]);
-#pragma unroll
-        for (int s = 0; s < KS / 2; ++s)
-          st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[s]),
-                                                       qb[half * KS / 2 + s], st, 0, 0, 0);
-      }
-      return st;
-    };
     // P = exp2(s * scale log2e - m) rounded to bf16 (the B operand of the PV product);
     // the row sum adds the fp32 values in a tree of v_add_f32.  (v_dot2_f32_bf16 on the
     // rounded pairs would take half the instructions, but the dot unit is the matrix
