@@ -663,12 +663,25 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
 #pragma unroll
     for (int e = 0; e < PER_LANE; ++e) pre[u][e] = u < nparts ? src[u * acc_stride + e] : 0.f;
 
-  float mx = kNegInf;
-  for (int p = lane; p < nparts; p += 64) mx = fmaxf(mx, ml[p * ml_stride]);
+  // Part `lane`'s (m, l) pair (one 8-byte load) serves both passes below; parts from 64 on
+  // (a sequence over more than 64 stream waves) are read again in the second.
+  float m0 = kNegInf, l0 = 0.f;
+  if (lane < nparts) {
+    const float2 v = *reinterpret_cast<const float2*>(ml + lane * ml_stride);
+    m0 = v.x;
+    l0 = v.y;
+  }
+  float mx = m0;
+  for (int p = lane + 64; p < nparts; p += 64) mx = fmaxf(mx, ml[p * ml_stride]);
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, xor_shfl(mx, o));
   float den = 0.f;
-  for (int p = lane; p < nparts; p += 64) {
+  if (lane < nparts) {
+    const float w = (m0 == kNegInf || mx == kNegInf) ? 0.f : fast_exp2(m0 - mx);
+    wsh[lane] = w;
+    den += w * l0;
+  }
+  for (int p = lane + 64; p < nparts; p += 64) {
     const float mp = ml[p * ml_stride];
     const float w = (mp == kNegInf || mx == kNegInf) ? 0.f : fast_exp2(mp - mx);
     wsh[p] = w;
