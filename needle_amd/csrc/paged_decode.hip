@@ -4,11 +4,12 @@
 // sequence gather K/V blocks, expand the GQA group, softmax(q K^T * scale) V.
 //
 // Work split (stream-K): for each kv head, the 16-token tiles of all sequences are
-// laid end to end (sequence i owns tiles P_i .. P_i + n_i, n_i = ceil(L_i / 16)),
-// and wave s of the kv head takes the C consecutive tiles s*C .. s*C + C, whatever
-// sequences they belong to.  Every wave has the same amount of K/V to stream, so
-// all of them run for the whole launch (a per-sequence split leaves the waves of
-// short remainders idle while the long ones finish).  The (wave s, sequence i)
+// laid end to end, each sequence after one empty slot (sequence i owns slots
+// P_i .. P_i + 1 + n_i, n_i = ceil(L_i / 16)), and wave s of the kv head takes the C
+// consecutive slots s*C .. s*C + C, whatever sequences they belong to.  Every wave has
+// about the same amount of K/V to stream (the empty slot stands for the cost of starting
+// a sequence), so all of them run for the whole launch (a per-sequence split leaves the
+// waves of short remainders idle while the long ones finish).  The (wave s, sequence i)
 // piece of a sequence that spans waves leaves partial (m, l, unnormalised acc) in
 // segment slot s + i of its kv head (unique: the waves and the sequences are both
 // in stream order); a sequence inside one wave is written directly.  A wave finds
@@ -108,6 +109,14 @@ __device__ __forceinline__ int seq_tiles(const DecodeArgs& a, int q) {
   return L <= 0 ? 0 : (int)((L + 15) >> 4);
 }
 
+// Stream slots of a sequence with n tiles: kStreamPad empty slots, then its tiles (none for
+// a sequence with nothing to attend).  The empty slots stand for what a wave spends on
+// starting a sequence (its q rows, its table window and its first block load before any
+// tile computes), so that the waves that cross a sequence boundary take fewer tiles and
+// finish with the others.
+constexpr int kStreamPad = 1;
+__device__ __forceinline__ int stream_slots(int n) { return n > 0 ? n + kStreamPad : 0; }
+
 // Inclusive prefix sum over the 64 lanes of a wave.
 __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
 #pragma unroll
@@ -118,21 +127,22 @@ __device__ __forceinline__ int wave_incl_scan(int v, int lane) {
   return v;
 }
 
-// Stream position of sequence `target`'s first tile, or of the first sequence that
-// owns tile `tile` (target < 0).  Sequences are scanned 64 at a time; the scan stops at
-// the chunk that holds the answer.  Returns the sequence in *seq (num_seqs if none) and
-// its first tile in *first.
+// Stream position of sequence `target`'s first slot, or of the first sequence whose slots
+// reach past stream slot `tile` (target < 0).  Sequences are scanned 64 at a time; the scan
+// stops at the chunk that holds the answer.  Returns the sequence in *seq (num_seqs if none) and
+// its first slot in *first.
 __device__ __forceinline__ void stream_locate(const DecodeArgs& a, int lane, int target,
                                               int64_t tile, int* seq, int64_t* first) {
   int64_t carry = 0;
   for (int base = 0; base < a.num_seqs; base += 64) {
     const int q = base + lane;
     const int n = q < a.num_seqs ? seq_tiles(a, q) : 0;
-    const int incl = wave_incl_scan(n, lane);
-    const int64_t excl = carry + incl - n;
+    const int v = stream_slots(n);
+    const int incl = wave_incl_scan(v, lane);
+    const int64_t excl = carry + incl - v;
     const uint64_t hit = target >= 0
         ? __builtin_amdgcn_ballot_w64(q == target)
-        : __builtin_amdgcn_ballot_w64(q < a.num_seqs && n > 0 && excl + n > tile);
+        : __builtin_amdgcn_ballot_w64(q < a.num_seqs && n > 0 && excl + v > tile);
     if (hit) {
       const int l = __builtin_ctzll(hit);
       *seq = base + l;
@@ -145,9 +155,9 @@ __device__ __forceinline__ void stream_locate(const DecodeArgs& a, int lane, int
   *first = carry;
 }
 
-// Tiles per wave: the fixed chunk, or the stream length (tiles of all sequences of one
+// Slots per wave: the fixed chunk, or the stream length (slots of all sequences of one
 // kv head) over the waves of a kv head, at least kDecodeMinChunk.
-// The chunk for a stream of `total` tiles.
+// The chunk for a stream of `total` slots.
 __device__ __forceinline__ int64_t stream_chunk_of(const DecodeArgs& a, int64_t total) {
   if (a.chunk > 0) return a.chunk;
   const int64_t c = (total + a.waves - 1) / a.waves;
@@ -159,12 +169,12 @@ __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
   for (int base = 0; base < a.num_seqs; base += 64) {
     const int q = base + lane;
     const int n = q < a.num_seqs ? seq_tiles(a, q) : 0;
-    total += __builtin_amdgcn_readlane(wave_incl_scan(n, lane), 63);
+    total += __builtin_amdgcn_readlane(wave_incl_scan(stream_slots(n), lane), 63);
   }
   return stream_chunk_of(a, total);
 }
 
-// NW == 1: one wave per workgroup, wave s of a kv head takes stream tiles s*C .. s*C + C.
+// NW == 1: one wave per workgroup, wave s of a kv head takes stream slots s*C .. s*C + C.
 // NW > 1: one workgroup per (kv head, sequence); wave w takes tiles w, w + NW, .. of the
 // sequence and the waves combine through LDS.
 // Two waves per SIMD for the default two-deep stream kernel (its 256-register budget), so
@@ -488,14 +498,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     int seq;
     if (one_load) {
       n_lane = lane < a.num_seqs ? seq_tiles(a, lane) : 0;
-      const int incl = wave_incl_scan(n_lane, lane);
+      const int v_lane = stream_slots(n_lane);
+      const int incl = wave_incl_scan(v_lane, lane);
       const int total = __builtin_amdgcn_readlane(incl, 63);
       chunk = stream_chunk_of(a, total);
       const int64_t tile = (int64_t)sw * chunk;
       const uint64_t hit = __builtin_amdgcn_ballot_w64(lane < a.num_seqs && n_lane > 0 &&
                                                        (int64_t)incl > tile);
       seq = hit ? __builtin_ctzll(hit) : a.num_seqs;
-      first = hit ? __builtin_amdgcn_readlane(incl - n_lane, seq) : total;
+      first = hit ? __builtin_amdgcn_readlane(incl - v_lane, seq) : total;
     } else {
       chunk = stream_chunk(a, lane);
       stream_locate(a, lane, -1, (int64_t)sw * chunk, &seq, &first);
@@ -504,11 +515,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     while (seq < a.num_seqs && first < end) {
       const int nt = one_load ? __builtin_amdgcn_readlane(n_lane, seq) : seq_tiles(a, seq);
       if (nt > 0) {
-        const int64_t s0 = start > first ? start : first;
-        const int64_t s1 = end < first + nt ? end : first + nt;
-        segment(seq, (int)(s0 - first), (int)(s1 - first), nt, sw + seq, nullptr);
+        const int64_t t0 = first + kStreamPad;   // the sequence's first tile
+        const int64_t s0 = start > t0 ? start : t0;
+        const int64_t s1 = end < t0 + nt ? end : t0 + nt;
+        if (s1 > s0) segment(seq, (int)(s0 - t0), (int)(s1 - t0), nt, sw + seq, nullptr);
       }
-      first += nt;
+      first += stream_slots(nt);
       ++seq;
     }
     if (held_seg >= 0) store_partial(held_seg, held, held_m, held_l);
@@ -633,10 +645,11 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   for (int base = 0; base < a.num_seqs; base += 64) {
     const int q = base + lane;
     const int n = q < a.num_seqs ? seq_tiles(a, q) : 0;
-    const int incl = wave_incl_scan(n, lane);
-    if (seq >= base && seq < base + 64) {
+    const int v = stream_slots(n);
+    const int incl = wave_incl_scan(v, lane);
+    if (seq >= base && seq < base + 64) {   // the sequence's tile count and first tile
       nt = __builtin_amdgcn_readlane(n, seq - base);
-      first = total + __builtin_amdgcn_readlane(incl - n, seq - base);
+      first = total + __builtin_amdgcn_readlane(incl - v, seq - base) + kStreamPad;
     }
     total += __builtin_amdgcn_readlane(incl, 63);
   }
@@ -811,7 +824,8 @@ inline int decode_layout(int num_seqs, int num_heads, int num_kv_heads, int head
   if (partition_tokens > 0) {
     if (partition_tokens % 16 != 0) return NDL_ERR_INVALID_ARG;
     lay->chunk = partition_tokens / 16;
-    lay->waves = ((int64_t)num_seqs * max_blocks + lay->chunk - 1) / lay->chunk;
+    // stream slots: every sequence's tiles and its kStreamPad empty slots
+    lay->waves = ((int64_t)num_seqs * (max_blocks + kStreamPad) + lay->chunk - 1) / lay->chunk;
   } else {
     int64_t resident = decode_resident_waves(
         head_dim == 128 ? decode_kernel_fn<128>(decode_pipeline_depth())

@@ -45,11 +45,12 @@ def test_version_and_status_text(lib):
 
 
 def test_decode_workspace_sizing(lib):
-    # 2 sequences x 32 heads over 8 kv heads, W = 64 blocks, 256 tokens (16 tiles) per
-    # wave -> ceil(2 * 64 / 16) = 8 waves per kv head, 8 + 2 segment slots per kv head,
+    # 2 sequences x 32 heads over 8 kv heads, W = 64 blocks, 256 tokens (16 stream slots)
+    # per wave; each sequence takes its tiles and one empty slot of the stream
+    # -> ceil(2 * (64 + 1) / 16) = 9 waves per kv head, 9 + 2 segment slots per kv head,
     # one (m, l) pair and one head_dim row per (kv head, segment, group head).
     n = lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 256)
-    slots = 8 * (8 + 2) * 4
+    slots = 8 * (9 + 2) * 4
     ml = (slots * 2 * 4 + 255) // 256 * 256
     assert n == ml + slots * 128 * 4
     # automatic split, stream form (a table of 257 blocks needs more than 16 tiles per
