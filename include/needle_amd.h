@@ -133,7 +133,8 @@ int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stride,
  * arguments and the device, 0 for an invalid shape).  partition_tokens selects the
  * split: 0 lets the library choose; -1 asks for one workgroup per (kv head, sequence)
  * whose waves combine their pieces on chip (the workspace is then a nominal 256 bytes);
- * a positive multiple of 16 asks for the stream split with that many tokens per wave.
+ * a positive multiple of 16 asks for the stream split with partition_tokens / 16 stream
+ * slots per wave (a slot is one 16-token tile; each sequence starts with one empty slot).
  * Pass the same value to ndl_paged_decode.
  */
 size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_heads,
