@@ -49,7 +49,8 @@ def run_oracle(case):
 
 
 # partition_tokens: 0 automatic, -1 one 8-wave workgroup per (kv head, sequence), > 0 the
-# stream split with that many tokens per wave.
+# stream split with partition_tokens / 16 stream slots per wave (16 tokens each; every
+# sequence starts with one empty slot, so at 16 some waves hold no tile at all).
 @pytest.mark.parametrize("part", [0, -1, 256])
 @pytest.mark.parametrize("cfg", ["qwen2-0.5b-decode", "llama3-8b-decode"])
 def test_decode_named_cases_vs_oracle(cfg, part):
