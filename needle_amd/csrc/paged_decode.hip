@@ -81,7 +81,7 @@ struct DecodeArgs {
   int group;
   float scale_log2;
   int num_seqs;
-  int chunk;      // C: tiles per wave; 0: ceil(T / waves) from the stream length T
+  int chunk;      // C: stream slots per wave; 0: ceil(T / waves) from the stream length T
   int waves;      // waves per kv head
   int nseg;       // segment slots per kv head: waves per kv head + num_seqs
   float* ws_ml;   // [kv head][segment][group head][2] = (m, l)
@@ -782,7 +782,7 @@ inline const void* pick_decode_kernel(int head_dim, bool app, bool rope, bool se
 
 struct DecodeLayout {
   int seq_split;        // waves per (kv head, sequence) workgroup, or 0 for the stream split
-  int64_t chunk;        // fixed tiles per wave, or 0 (from the stream length on the device)
+  int64_t chunk;        // fixed stream slots per wave, or 0 (from the stream length on the device)
   int64_t waves;        // waves per kv head
   int64_t nseg;         // segment slots per kv head
   size_t ml_bytes;      // (m, l) region, 256-byte aligned
