@@ -15,14 +15,23 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 
+def prefill_flags():
+    """The extra compiler flags the Makefile gives varlen_prefill.hip (PREFILL_FLAGS)."""
+    with open(os.path.join(ROOT, "needle_amd", "csrc", "Makefile")) as f:
+        for line in f:
+            if line.startswith("PREFILL_FLAGS"):
+                return line.split(":=", 1)[1].split()
+    return []
+
+
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
 def test_prefill_kernels_use_m0_only_for_direct_lds_loads(tmp_path):
     src = os.path.join(ROOT, "needle_amd", "csrc", "varlen_prefill.hip")
     asm = tmp_path / "vp.s"
     subprocess.check_call([HIPCC, "--offload-arch=gfx950", "-O3", "-std=c++17", "-Xclang",
                            "-target-feature", "-Xclang", "-packed-fp32-ops",
-                           "-I" + os.path.join(ROOT, "include"), "-S", "--cuda-device-only",
-                           src, "-o", str(asm)], stderr=subprocess.DEVNULL)
+                           "-I" + os.path.join(ROOT, "include"), *prefill_flags(), "-S",
+                           "--cuda-device-only", src, "-o", str(asm)], stderr=subprocess.DEVNULL)
     lines = asm.read_text().splitlines()
     kernels = [i for i, l in enumerate(lines)
                if re.match(r"_ZN3ndl21varlen_prefill_kernel.*:", l)]
