@@ -90,6 +90,18 @@ def test_shapes_and_edge_lengths(shape):
     assert_close(got, want)
 
 
+@pytest.mark.parametrize("shape", [wl.QWEN2_7B, wl.QWEN2_05B])
+def test_empty_prompts_between_real_ones(shape):
+    """Zero-length prompts (equal consecutive cu_seqlens entries) at the start, in the middle
+    and at the end of the batch own no rows and no tile; the prompts around them attend only
+    their own blocks, and the pool matches the oracle's append byte for byte."""
+    case = wl.prefill_case(shape, [0, 17, 0, 0, 300, 0, 33, 0], seed=310)
+    got, pool = run_gpu(case)
+    want, want_pool = oracle(case)
+    assert torch.equal(pool.view(torch.int16), want_pool.view(torch.int16))
+    assert_close(got, want)
+
+
 def test_single_token_prompts_return_value_rows():
     shape = wl.QWEN2_7B
     case = wl.prefill_case(shape, [1, 1, 1], seed=302)
