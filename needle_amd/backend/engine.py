@@ -2,7 +2,8 @@
 
 add_request / step / has_unfinished_requests / generate keep the reference's meaning: a
 request finishes when it emits a stop token or max_new_tokens tokens, and step() returns
-{request_id: generated token ids} for the requests that finished in that step.  The model
+{request_id: generated token ids} for the requests that finished in that step.  Sampling
+is greedy only: a request with temperature > 0 is refused when it is added.  The model
 comes from a ModelConfig with synthetic weights (no checkpoint loading) or is passed in.
 decode_graphs=True replays decode steps from HIP graphs captured per batch-size bucket;
 their metadata stays on the device between steps (sequences longer than max_model_len, or
@@ -18,6 +19,7 @@ import torch
 
 from ..model.config import ModelConfig
 from ..model.runner import ModelRunner
+from ..model.sampler import check_greedy
 from .block_allocator import BlockAllocator
 from .request import SamplingParams, SeqState
 from .scheduler import Scheduler
@@ -48,6 +50,7 @@ class LLMEngine:
 
     def add_request(self, request_id: str, prompt_token_ids: List[int],
                     sampling_params: SamplingParams) -> None:
+        check_greedy(sampling_params)
         self.scheduler.add(SeqState(next(self._ids), request_id, list(prompt_token_ids),
                                     sampling_params))
 
@@ -69,7 +72,8 @@ class LLMEngine:
     def generate(self, prompt_token_ids: List[int],
                  sampling_params: Optional[SamplingParams] = None,
                  request_id: str = "sync-0") -> List[int]:
-        self.add_request(request_id, prompt_token_ids, sampling_params or SamplingParams())
+        self.add_request(request_id, prompt_token_ids,
+                         sampling_params or SamplingParams(temperature=0.0))
         while self.has_unfinished_requests():
             done = self.step()
             if request_id in done:

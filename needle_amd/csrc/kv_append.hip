@@ -187,7 +187,9 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
                   &bt_row_stride, &max_blocks_per_seq, &cu_seqlens, &context_lens, &num_seqs,
                   &num_tokens};
   if (hipLaunchKernel(fns[small ? 1 : 0][tpw - 1], dim3((unsigned)blocks), dim3(256), args, 0,
-                      (hipStream_t)stream) != hipSuccess)
+                      (hipStream_t)stream) != hipSuccess) {
+    (void)hipGetLastError();  // clear the error so that the next call's check sees its own
     return NDL_ERR_LAUNCH;
+  }
   return check_launch();
 }

@@ -16,8 +16,7 @@ How this runner feeds the device:
     greedy tokens are written into the next step's input ids inside the graph, and the
     host sends only what changed (context lengths, new rows, new blocks) as one small
     scatter.  Padding rows point at a scratch block the allocator never hands out;
-  * greedy sampling is one device argmax and one host copy for the whole batch; other
-    rows go through needle_amd.model.sampler;
+  * sampling is greedy: one device argmax and one host copy for the whole batch;
   * swapping moves every block of every layer in one ndl_kv_block_copy launch per
     direction (the reference issues one copy per layer and block, runner.py:175-192).
 """
@@ -34,7 +33,7 @@ from ..backend.request import SeqState
 from ..backend.scheduler import StepPlan
 from .config import ModelConfig
 from .qwen2 import build_model, random_init_
-from .sampler import sample
+from .sampler import check_greedy, sample
 
 
 @dataclass
@@ -59,6 +58,12 @@ class _DecodeRows:
     Every step the host sends (flat index, value) pairs for what changed and applies them
     with one scatter: the context lengths of the live rows, the rows that were filled, the
     block ids a sequence gained.  The tokens of greedy rows are written by the graph itself.
+
+    A sequence's block list is either grown by append (a new block at a block edge) or
+    replaced by a new list object (admission, swap-out, swap-in, release): the scheduler
+    never rewrites one in place.  A row whose sequence holds a different list object than
+    at the last sync (it was swapped or recomputed while the steps in between ran eagerly)
+    is sent whole again.
     """
 
     def __init__(self, capacity: int, width: int, scratch_block: int, device):
@@ -70,6 +75,7 @@ class _DecodeRows:
         self.table.fill_(scratch_block)
         self.rows: List[SeqState] = []
         self.sent_blocks: List[int] = []     # table entries the device holds, per row
+        self.sent_list: List[Optional[List[int]]] = []  # the block list they came from
         self.dirty: List[bool] = []          # row refilled: send all of it
         self.tok_on_device: List[bool] = []  # the graph wrote this row's newest token
         self._staging: List[torch.Tensor] = []
@@ -109,6 +115,7 @@ class _DecodeRows:
                 self.tok_on_device[r] = False
             self.rows.pop()
             self.sent_blocks.pop()
+            self.sent_list.pop()
             self.dirty.pop()
             self.tok_on_device.pop()
         # arriving sequences take the rows after the last one (all padding on the device)
@@ -117,20 +124,23 @@ class _DecodeRows:
             if id(s) not in present:
                 self.rows.append(s)
                 self.sent_blocks.append(0)
+                self.sent_list.append(None)
                 self.dirty.append(True)
                 self.tok_on_device.append(False)
         for r, s in enumerate(self.rows):
             base = 2 * cap + r * w
             nb = len(s.blocks)
             sent = self.sent_blocks[r]
-            if self.dirty[r]:
-                for j in range(nb, sent):              # the previous occupant's extra entries
+            if self.dirty[r] or self.sent_list[r] is not s.blocks or nb < sent:
+                # a refilled row, or a block list replaced since the last sync
+                for j in range(nb, sent):              # entries past the new list's end
                     upd[base + j] = self.scratch
                 sent = 0
                 self.dirty[r] = False
             for j in range(sent, nb):
                 upd[base + j] = s.blocks[j]
             self.sent_blocks[r] = nb
+            self.sent_list[r] = s.blocks
             upd[cap + r] = s.length - 1
             if not (self.tok_on_device[r] and s.params.greedy):
                 upd[r] = s.last_token
@@ -331,6 +341,8 @@ class ModelRunner:
         rows = self._rows
         if not rows.fits(seqs, self.block_size):
             return None
+        for s in seqs:
+            check_greedy(s.params)
         b = len(seqs)
         bucket = next((k for k in sorted(self._graphs) if k >= b), None)
         if bucket is None:
@@ -344,10 +356,6 @@ class ModelRunner:
         where = rows.row_of()
         order = [where[id(s)] for s in seqs]
         out = [greedy[r] for r in order]
-        if not all(s.params.greedy for s in seqs):
-            picks = sample(logits[torch.tensor(order, device=self.device)],
-                           [s.params for s in seqs])
-            out = [t if s.params.greedy else p for s, t, p in zip(seqs, out, picks)]
         for r in range(b):
             rows.tok_on_device[r] = True
         return out

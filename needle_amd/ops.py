@@ -319,6 +319,11 @@ def varlen_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.T
     n_tok = q.shape[0]
     if out is None:
         out = torch.empty((n_tok, num_heads, head_dim), dtype=q.dtype, device=dev)
+    else:
+        _require(out.shape == (n_tok, num_heads, head_dim) and out.is_contiguous()
+                 and out.dtype == q.dtype and out.device == dev,
+                 f"out must be a contiguous {q.dtype} [{n_tok}, {num_heads}, {head_dim}] "
+                 f"tensor on {dev}")
     if n_tok == 0 or n_seqs == 0:
         return out
     _require(block_table.shape[1] > 0, "block_table has no columns")

@@ -2,6 +2,7 @@
 bookkeeping of the device-resident decode rows (run against a CPU buffer here)."""
 import random
 
+import pytest
 import torch
 
 from needle_amd.backend.request import SamplingParams, SeqState
@@ -10,15 +11,14 @@ from needle_amd.model.runner import ModelRunner, _DecodeRows
 from needle_amd.model.sampler import sample
 
 
-def test_greedy_and_degenerate_stochastic_rows_agree():
+def test_greedy_sampling_and_refused_stochastic_rows():
     torch.manual_seed(0)
     logits = torch.randn(5, 50)
     want = logits.argmax(-1).tolist()
     assert sample(logits, [SamplingParams(temperature=0.0)] * 5) == want
-    g = torch.Generator().manual_seed(1)
-    # top_k = 1 (and a tiny top_p) leave only the argmax
-    assert sample(logits, [SamplingParams(temperature=0.7, top_k=1)] * 5, g) == want
-    assert sample(logits, [SamplingParams(temperature=0.7, top_p=1e-6)] * 5, g) == want
+    for p in (SamplingParams(), SamplingParams(temperature=0.7, top_k=1)):
+        with pytest.raises(NotImplementedError):
+            sample(logits, [SamplingParams(temperature=0.0)] * 4 + [p])
 
 
 def test_sampling_params_reject_out_of_range_values():
@@ -125,3 +125,26 @@ def test_decode_rows_fit_rules():
     long = _seq(2, list(range(40)), blocks=[1, 2, 3])
     assert rows.fits([short], 16) and not rows.fits([long], 16)
     assert not rows.fits([short] * 5, 16)
+
+
+def test_decode_rows_resend_a_replaced_block_list():
+    """A sequence keeps its row while the steps in between run eagerly (no sync), and its
+    block list is replaced meanwhile (swap-out and swap-in, or a recompute): the next sync
+    must send the new ids, not only the entries past the old count."""
+    rows = _DecodeRows(4, 6, 99, "cpu")
+    a = _seq(1, list(range(40)), blocks=[1, 2, 3])
+    b = _seq(2, list(range(20)), blocks=[4, 5])
+    rows.sync([a, b])
+    a.blocks = [10, 11, 12]                       # swapped out and back into other blocks
+    b.blocks = [7]                                # recomputed into a shorter list
+    b.tokens = b.tokens[:10]
+    rows.forget_tokens()                          # the eager steps in between
+    rows.sync([a, b])
+    tok, ctx, tab = _expect(rows, [a, b], rows.tok.clone())
+    assert torch.equal(rows.table, tab) and torch.equal(rows.ctx, ctx)
+    assert rows.table[rows.row_of()[id(b)]].tolist() == [7, 99, 99, 99, 99, 99]
+    # growth by append on the same list is still sent incrementally
+    a.blocks.append(13)
+    a.tokens += [0] * 16
+    rows.sync([a, b])
+    assert rows.table[rows.row_of()[id(a)]].tolist() == [10, 11, 12, 13, 99, 99]

@@ -16,12 +16,11 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
 
 def prefill_flags():
-    """The extra compiler flags the Makefile gives varlen_prefill.hip (PREFILL_FLAGS)."""
-    with open(os.path.join(ROOT, "needle_amd", "csrc", "Makefile")) as f:
-        for line in f:
-            if line.startswith("PREFILL_FLAGS"):
-                return line.split(":=", 1)[1].split()
-    return []
+    """The extra compiler flags the Makefile gives varlen_prefill.hip (PREFILL_FLAGS, which
+    the Makefile keeps only when this toolchain accepts them)."""
+    out = subprocess.check_output(["make", "-s", "-C", os.path.join(ROOT, "needle_amd", "csrc"),
+                                   "print-prefill-flags"], text=True)
+    return out.split()
 
 
 @pytest.mark.skipif(not os.path.exists(HIPCC), reason="hipcc not installed")
