@@ -213,11 +213,13 @@ def e2e_measurement(torch, time_limit_s):
 
 
 def e2e_cpu_subset(torch, n_requests=8, max_new=32):
-    """The end-to-end subset on both paths: the GPU engine runs the first n_requests of the
-    benchmark (outputs capped at max_new), then a CPU runner with the same weights whose
-    attention seams are the oracle (the reference torch path) replays the same schedule
-    teacher-forced with the GPU's tokens.  Reports the CPU path's output tok/s on that
-    subset and how often its greedy pick agrees with the GPU's."""
+    """The end-to-end subset on both paths: the benchmark's engine (e2e.build_engine: decode
+    steps replayed from HIP graphs over device-resident rows, the path the end-to-end figure
+    times) runs the first n_requests of the benchmark (outputs capped at max_new), then a
+    CPU runner with the same weights whose attention seams are the oracle (the reference
+    torch path) replays the same schedule teacher-forced with the GPU's tokens.  Reports
+    the CPU path's output tok/s on that subset and how often its greedy pick agrees with
+    the graph-replayed GPU engine's."""
     import copy
     import types
     from needle_amd import e2e
@@ -233,7 +235,28 @@ def e2e_cpu_subset(torch, n_requests=8, max_new=32):
     base = random_init_(build_model(cfg), e2e.E2E_SEED)
     reqs = [(rid, p, min(o, max_new)) for rid, p, o in e2e.requests(n_requests)]
     nb = 2048
-    gpu = ModelRunner(cfg, device="cuda:0", model=copy.deepcopy(base))
+    schedule = []                   # per step: the GPU engine's tokens, plan.seqs order
+    engine = e2e.build_engine(max_gpu_blocks=nb, model=copy.deepcopy(base))
+    for rid, prompt, olen in reqs:
+        engine.add_request(rid, prompt, SamplingParams(temperature=0.0, max_new_tokens=olen))
+    graph_steps = 0
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    while engine.has_unfinished_requests():
+        plan = engine.scheduler.schedule()
+        rn = engine.runner
+        graph_steps += bool(plan.decode) and len(plan.decode) <= max(rn._graphs) and \
+            rn._rows.fits(plan.decode, rn.block_size)
+        toks = engine.runner.execute(plan)
+        schedule.append(toks)
+        for s, t in zip(plan.seqs, toks):
+            if s.push(t):
+                engine.scheduler.finish(s)
+    gpu_s = time.perf_counter() - t0
+    gpu_tok = sum(len(t) for t in schedule)
+    del engine
+    torch.cuda.empty_cache()
+
     cpu = ModelRunner(cfg, device="cpu", model=base)
     for layer in cpu.model.model.layers:
         att = layer.self_attn
@@ -245,49 +268,40 @@ def e2e_cpu_subset(torch, n_requests=8, max_new=32):
             lambda self, q, k, v, kv, bt, ctx: paged_ref.decode(
                 q, k, v, kv, bt, ctx, self.scale, self.num_heads, self.num_kv_heads,
                 self.head_dim), att)
-    results = {}
-    schedule = []                   # per step: [(group, is_prefill, gpu tokens)]
-    for side, runner in (("gpu", gpu), ("cpu", cpu)):
-        runner.init_kv_cache(nb)
-        sched = Scheduler(BlockAllocator(nb, 0, 16), 256, 8192)
-        for i, (rid, prompt, olen) in enumerate(reqs):
-            sched.add(SeqState(i + 1, rid, prompt, SamplingParams(temperature=0.0,
-                                                                  max_new_tokens=olen)))
-        n_tok, agree, step = 0, 0, 0
-        if side == "gpu":
-            torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        while sched.pending():
-            plan = sched.schedule()
-            toks = []
-            for group, pre in ((plan.prefill, True), (plan.decode, False)):
-                if group:
-                    lg = runner.forward(runner.prepare_inputs(group, pre))
-                    toks += lg.argmax(-1).tolist()
-            for s in plan.prefill:
-                s.kv_ready = True
-            if side == "gpu":
-                schedule.append(toks)
-                forced = toks
-            else:
-                forced = schedule[step]
-                agree += sum(a == b for a, b in zip(toks, forced))
-            for s, t in zip(plan.seqs, forced):
-                n_tok += 1
-                if s.push(t):
-                    sched.finish(s)
-            step += 1
-        el = time.perf_counter() - t0
-        results[side] = (n_tok, el, agree)
-    del gpu
-    torch.cuda.empty_cache()
-    n_tok, el, agree = results["cpu"]
+    cpu.init_kv_cache(nb)
+    # the engine keeps its last block for the graphs' padding rows: same allocator size here
+    sched = Scheduler(BlockAllocator(nb - 1, 0, 16), 256, 8192)
+    for i, (rid, prompt, olen) in enumerate(reqs):
+        sched.add(SeqState(i + 1, rid, prompt, SamplingParams(temperature=0.0,
+                                                              max_new_tokens=olen)))
+    n_tok = agree = step = 0
+    t0 = time.perf_counter()
+    while sched.pending():
+        plan = sched.schedule()
+        toks = []
+        for group, pre in ((plan.prefill, True), (plan.decode, False)):
+            if group:
+                toks += cpu.forward(cpu.prepare_inputs(group, pre)).argmax(-1).tolist()
+        for s in plan.prefill:
+            s.kv_ready = True
+        forced = schedule[step]
+        agree += sum(a == b for a, b in zip(toks, forced))
+        for s, t in zip(plan.seqs, forced):
+            n_tok += 1
+            if s.push(t):
+                sched.finish(s)
+        step += 1
+    el = time.perf_counter() - t0
+    if step != len(schedule) or n_tok != gpu_tok:
+        raise RuntimeError("the CPU schedule diverged from the GPU engine's")
     return {"value": round(n_tok / el, 2), "unit": "output tok/s",
             "kind": "port", **host_info(torch),
             "sample": f"the first {n_requests} benchmark requests, outputs capped at {max_new} "
                       f"tokens ({n_tok} tokens, {el:.1f} s), eager CPU runner with the oracle "
-                      "attention seams, teacher-forced with the GPU engine's tokens",
-            "gpu_eager_tok_per_s_same_subset": round(results["gpu"][0] / results["gpu"][1], 1),
+                      "attention seams, teacher-forced with the graph-replayed GPU engine's "
+                      "tokens",
+            "gpu_engine_tok_per_s_same_subset": round(gpu_tok / gpu_s, 1),
+            "gpu_graph_decode_steps": graph_steps,
             "greedy_agreement": round(agree / max(1, n_tok), 4)}
 
 
