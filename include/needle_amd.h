@@ -50,7 +50,7 @@ extern "C" {
 /* Same object as hipStream_t; declared here so callers need no HIP headers. */
 typedef struct ihipStream_t* ndl_stream_t;
 
-#define NDL_ABI_VERSION 4
+#define NDL_ABI_VERSION 5
 
 enum ndl_status {
   NDL_OK = 0,
@@ -58,7 +58,8 @@ enum ndl_status {
   NDL_ERR_UNSUPPORTED = -2,   /* dtype / head_dim / block_size / group size not built */
   NDL_ERR_WORKSPACE = -3,     /* workspace smaller than the *_workspace_bytes query */
   NDL_ERR_LAUNCH = -4,        /* the HIP runtime rejected a kernel launch */
-  NDL_ERR_SCRATCH_LIMIT = -5  /* the shape needs more than NDL_DECODE_STATIC_SCRATCH_BYTES */
+  NDL_ERR_SCRATCH_LIMIT = -5, /* the shape needs more than NDL_DECODE_STATIC_SCRATCH_BYTES */
+  NDL_ERR_CAPTURE = -6        /* a device's first allocation-free call made under capture */
 };
 
 /* Size of the per-device static scratch array of ndl_paged_decode_append_noalloc. */
@@ -233,7 +234,10 @@ int ndl_rope_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
  * overlap on one GPU (different streams, or different host threads without stream order
  * between them) race and may return wrong results; calls in stream order are safe.  The
  * first call on a device looks the array's address up (hipGetSymbolAddress) with that
- * device current.
+ * device current; that lookup may load the library's code object, which allocates, so it
+ * must not happen while `stream` is being captured: such a call returns NDL_ERR_CAPTURE
+ * and enqueues nothing.  A call with num_seqs = 0 (pointers unused) does only the lookup,
+ * so a caller that captures makes one before its first capture on each device.
  */
 int ndl_paged_decode_append_noalloc(void* out, const void* q, int64_t q_tok_stride,
                                     const void* k, int64_t k_tok_stride,

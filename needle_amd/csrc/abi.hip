@@ -11,6 +11,8 @@ extern "C" const char* ndl_strerror(int status) {
     case NDL_ERR_WORKSPACE: return "workspace missing or too small";
     case NDL_ERR_LAUNCH: return "kernel launch failed";
     case NDL_ERR_SCRATCH_LIMIT: return "shape needs more than the static decode scratch";
+    case NDL_ERR_CAPTURE:
+      return "first allocation-free call on this device made under stream capture";
     default: return "unknown status";
   }
 }

@@ -878,8 +878,9 @@ static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kStaticScratchDevices] = {};
 
 // The device address of `scratch` on the current device (looked up on the first call per
-// device, with that device current).
-static int static_scratch_ptr(void** ptr) {
+// device, with that device current).  The lookup can load the code object, which allocates:
+// refused while `stream` is being captured.
+static int static_scratch_ptr(hipStream_t stream, void** ptr) {
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess) {
     (void)hipGetLastError();
@@ -888,6 +889,12 @@ static int static_scratch_ptr(void** ptr) {
   if (dev < 0 || dev >= kStaticScratchDevices) return NDL_ERR_UNSUPPORTED;
   std::lock_guard<std::mutex> lock(g_scratch_mu);
   if (g_scratch_ptr[dev] == nullptr) {
+    hipStreamCaptureStatus capturing = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(stream, &capturing) != hipSuccess) {
+      (void)hipGetLastError();
+      return NDL_ERR_LAUNCH;
+    }
+    if (capturing != hipStreamCaptureStatusNone) return NDL_ERR_CAPTURE;
     void* p = nullptr;
     if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || p == nullptr) {
       (void)hipGetLastError();
@@ -919,7 +926,8 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   if (num_seqs < 0 || num_blocks <= 0 || max_blocks_per_seq <= 0 ||
       bt_row_stride < max_blocks_per_seq || q_tok_stride < (int64_t)num_heads * head_dim)
     return NDL_ERR_INVALID_ARG;
-  if (num_seqs == 0) return NDL_OK;
+  if (num_seqs == 0)  // nothing to do; the allocation-free form looks its array up
+    return static_scratch ? static_scratch_ptr((hipStream_t)stream, &workspace) : NDL_OK;
   if (!out || !q || !kv_cache || !block_table || !context_lens) return NDL_ERR_INVALID_ARG;
   if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)kv_cache) & 15u) return NDL_ERR_INVALID_ARG;
   if (q_tok_stride & 7) return NDL_ERR_INVALID_ARG;
@@ -938,7 +946,7 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   if (grid_waves > 0x7fffffff || lay.nseg > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
   if (static_scratch) {
     if (lay.bytes > kStaticScratchBytes) return NDL_ERR_SCRATCH_LIMIT;
-    const int rc = static_scratch_ptr(&workspace);
+    const int rc = static_scratch_ptr((hipStream_t)stream, &workspace);
     if (rc != NDL_OK) return rc;
     workspace_bytes = kStaticScratchBytes;
   }

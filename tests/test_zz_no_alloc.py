@@ -71,3 +71,41 @@ def test_noalloc_per_sequence_workgroups():
     out_ws, pool_ws = _call(lib, case, use_static=False)
     out_st, pool_st = _call(lib, case, use_static=True)
     assert _same(out_ws, out_st) and _same(pool_ws, pool_st)
+
+
+def _args(case, out, part=0):
+    s = case.shape
+    return (out.data_ptr(), case.q.data_ptr(), s.num_heads * s.head_dim,
+            case.k.data_ptr(), s.num_kv_heads * s.head_dim,
+            case.v.data_ptr(), s.num_kv_heads * s.head_dim,
+            case.kv_cache.data_ptr(), case.num_blocks,
+            case.block_table.data_ptr(), case.block_table.stride(0), case.block_table.shape[1],
+            case.context_lens.data_ptr(), case.num_seqs, s.num_heads, s.num_kv_heads,
+            s.head_dim, s.block_size, _lib.NDL_DTYPE_BF16, ctypes.c_float(s.scale), part)
+
+
+def test_noalloc_replayed_from_a_graph():
+    """The callers this entry point is for capture it.  After one call outside capture (the
+    first on the device looks the array up), a captured call is replayed three times, with
+    eager work between the replays, and must equal the eager call every time."""
+    lib = _lib.load()
+    g = wl.config_case("llama3-8b-decode").to(DEV)
+    s = g.shape
+    out = torch.empty((g.num_seqs, s.num_heads, s.head_dim), dtype=torch.bfloat16, device=DEV)
+    _lib.check(lib.ndl_paged_decode_append_noalloc(
+        *_args(g, out), torch.cuda.current_stream().cuda_stream), "eager call")
+    torch.cuda.synchronize()
+    want_out, want_pool = out.clone(), g.kv_cache.clone()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.ndl_paged_decode_append_noalloc(*_args(g, out),
+                                                 torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "captured call")
+    x = torch.randn(1024, 1024, device=DEV)
+    for _ in range(3):
+        out.zero_()
+        y = x @ x
+        graph.replay()
+        torch.cuda.synchronize()
+        assert _same(out, want_out) and _same(g.kv_cache, want_pool)
+        del y
