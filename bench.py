@@ -419,11 +419,29 @@ def qwen7b_prefill(torch, ops, wl, reps, cpu=True):
     del g3r
     # q read and rotated q written, cos/sin read, plus the append's bytes
     rb = 2 * t3 * s3.num_heads * s3.head_dim * 2 + 2 * t3 * s3.head_dim * 2 + ab
+
+    # The drop-in layer's form: k rotated and appended alone, q rotated inside the prefill.
+    def rope3k_x10():
+        for _ in range(10):
+            ops.rope_kv_append(None, c3.k, c3.v, cos3, sin3, c3.kv_cache, c3.block_table,
+                               c3.context_lens, cu_seqlens=c3.cu_seqlens)
+    rope3k_x10()
+    g3k = capture(torch, rope3k_x10)
+    ms_rk = time_region(torch, g3k.replay, reps) / 10
+    del g3k
+    rkb = 2 * t3 * s3.head_dim * 2 + ab     # cos/sin read, plus the append's bytes
+
+    def att3_rope():
+        ops.varlen_prefill(c3.q, c3.kv_cache, c3.block_table, c3.cu_seqlens, c3.context_lens,
+                           c3.max_seqlen, s3.scale, s3.num_heads, s3.num_kv_heads, s3.head_dim,
+                           cos=cos3, sin=sin3)
     app3()   # the cache holds k again (the rotated rows only changed its values)
     # The prefill is compute-bound: its clock ramps over ~1 s of load, so it is timed right
-    # after 1.5 s of warm-up launches, over 50 launches.
+    # after 1.5 s of warm-up launches, over 50 launches (each form, then the first again).
     warm(torch, att3, 1.5)
     ms_p = time_region(torch, att3, 50)
+    ms_pr = time_region(torch, att3_rope, 50)
+    ms_p2 = time_region(torch, att3, 50)
     fl = wl.prefill_flops(s3, c3.new_lens)
     res = {
         "tokens": t3, "append_us": round(ms_a * 1e3, 2),
@@ -436,7 +454,20 @@ def qwen7b_prefill(torch, ops, wl, reps, cpu=True):
         "attention_tflops": round(fl / ms_p / 1e9, 1),
         "attention_frac_of_mfma_peak": round(fl / ms_p / 1e9 / MFMA_BF16_PEAK_TFLOPS, 4),
         "attention_launches_timed": 50,
-        "algorithmic_flops": fl}
+        "algorithmic_flops": fl,
+        "layer_prefill_path": {
+            "rope_q_and_k_append_then_prefill_us": round((ms_r + ms_p) * 1e3, 2),
+            "rope_k_append_then_rope_prefill_us": round((ms_rk + ms_pr) * 1e3, 2),
+            "rope_k_append_us": round(ms_rk * 1e3, 2),
+            "rope_k_append_gbs": round(rkb / ms_rk / 1e6, 1),
+            "rope_prefill_us": round(ms_pr * 1e3, 2),
+            "rope_prefill_tflops": round(fl / ms_pr / 1e9, 1),
+            "prefill_us_retimed_after": round(ms_p2 * 1e3, 2),
+            "q_round_trip_bytes_removed": 2 * t3 * s3.num_heads * s3.head_dim * 2,
+            "note": "the drop-in layer's prefill (RoPE + append + attention): before, "
+                    "ndl_rope_kv_append writes the rotated q and ndl_varlen_prefill reads it "
+                    "back; now ndl_rope_kv_append rotates k only and ndl_rope_varlen_prefill "
+                    "rotates each q row as it reads it"}}
     if cpu:
         cc = c3.to("cpu")
         t0 = time.perf_counter()

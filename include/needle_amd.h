@@ -18,6 +18,8 @@
  *   ndl_varlen_prefill  causal attention of packed varlen prompts, reading K/V
  *                       back through block_table
  *                       (_prefill_pytorch :120-134; FlashInfer path :109-118)
+ *   ndl_rope_varlen_prefill  the same with the rotary embedding of q folded in
+ *                       (q's half of :88, then :102-107)
  *   ndl_kv_block_copy   whole-block copies between pools for the KV swap
  *                       (needle/model/runner.py:175-192)
  *
@@ -117,7 +119,8 @@ int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int bloc
  * v unchanged go to the cache slot that ndl_kv_append would pick for token t
  * (same slot rule, same handling of out-of-range block ids).  cos/sin:
  * [num_tokens][head_dim] with token stride cs_tok_stride.  head_dim must be a
- * multiple of 16; bf16 only.
+ * multiple of 16; bf16 only.  q and q_out may both be NULL: then only k is rotated and
+ * k, v appended (for ndl_rope_varlen_prefill, which rotates q itself).
  */
 int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stride,
                        const void* k, int64_t k_tok_stride,
@@ -274,6 +277,30 @@ int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
                        int num_seqs, int64_t num_tokens, int max_seqlen, int max_context_len,
                        int num_heads, int num_kv_heads, int head_dim, int block_size, int dtype,
                        float scale, ndl_stream_t stream);
+
+/*
+ * ndl_varlen_prefill on the raw (not yet rotated) q: each query row is rotated as the
+ * kernel reads it, with the rounding of ndl_rope_kv_append, so out is bit-identical to
+ * ndl_rope_kv_append (q_out) followed by ndl_varlen_prefill on q_out, and no rotated q
+ * is written to or read back from memory.
+ *
+ * Replaces: needle/layers/attention.py:88 for q (_apply_rope, :277-288) together with
+ *           _prefill's attention (:102-107, _prefill_pytorch :120-134).
+ *
+ * cos, sin: [num_tokens][head_dim] (the rows of each packed token, as
+ * ndl_rope_kv_append takes them), token stride cs_tok_stride (a multiple of 8), 16-byte
+ * aligned.  K/V of the new tokens must already be in the cache, rotated: call
+ * ndl_rope_kv_append with q = q_out = NULL first.  Other arguments as ndl_varlen_prefill.
+ */
+int ndl_rope_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
+                            const void* cos, const void* sin, int64_t cs_tok_stride,
+                            const void* kv_cache, int64_t num_blocks,
+                            const int32_t* block_table, int64_t bt_row_stride,
+                            int max_blocks_per_seq, const int32_t* cu_seqlens,
+                            const int32_t* context_lens, int num_seqs, int64_t num_tokens,
+                            int max_seqlen, int max_context_len, int num_heads,
+                            int num_kv_heads, int head_dim, int block_size, int dtype,
+                            float scale, ndl_stream_t stream);
 
 /*
  * Copy whole KV blocks between two sets of per-layer pools: the swap-out (GPU pool ->

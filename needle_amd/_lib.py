@@ -32,6 +32,7 @@ EXPORTED_SYMBOLS = (
     "ndl_paged_decode_append_noalloc",
     "ndl_rope_paged_decode_append",
     "ndl_varlen_prefill",
+    "ndl_rope_varlen_prefill",
     "ndl_kv_block_copy",
 )
 
@@ -100,6 +101,15 @@ _SIGNATURES = {
     ]),
     "ndl_varlen_prefill": (_c_i32, [
         _c_p, _c_p, _c_i64,                             # out, q, q stride
+        _c_p, _c_i64,                                   # cache, NB
+        _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
+        _c_p, _c_p, _c_i32, _c_i64, _c_i32, _c_i32,     # cu, ctx, B, T, max_seqlen, max_ctx
+        _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # H, Hkv, D, bs, dtype
+        _c_f32, _c_p,                                   # scale, stream
+    ]),
+    "ndl_rope_varlen_prefill": (_c_i32, [
+        _c_p, _c_p, _c_i64,                             # out, q, q stride
+        _c_p, _c_p, _c_i64,                             # cos, sin, cos/sin stride
         _c_p, _c_i64,                                   # cache, NB
         _c_p, _c_i64, _c_i32,                           # block_table, row stride, W
         _c_p, _c_p, _c_i32, _c_i64, _c_i32, _c_i32,     # cu, ctx, B, T, max_seqlen, max_ctx

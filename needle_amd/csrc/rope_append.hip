@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
       (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int D = a.head_dim, half = D >> 1, cph = half >> 3;  // chunks per half row
   const int H = a.num_heads, Hkv = a.num_kv_heads, bs = a.block_size;
-  const int kv_items = 2 * Hkv * cph, q_items = H * cph;
+  const int kv_items = 2 * Hkv * cph, q_items = a.q != nullptr ? H * cph : 0;
   const int kv_rounds = (kv_items + 63) >> 6, rounds = kv_rounds + ((q_items + 63) >> 6);
   const int64_t t = w / rounds;
   const int r = (int)(w - t * rounds);
@@ -158,11 +158,11 @@ extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stri
       max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq)
     return NDL_ERR_INVALID_ARG;
   if (num_tokens == 0) return NDL_OK;
-  if (!q_out || !q || !k || !v || !cos || !sin || !kv_cache || !block_table || !context_lens ||
-      num_seqs == 0)
+  if ((q_out == nullptr) != (q == nullptr)) return NDL_ERR_INVALID_ARG;  // both or neither
+  if (!k || !v || !cos || !sin || !kv_cache || !block_table || !context_lens || num_seqs == 0)
     return NDL_ERR_INVALID_ARG;
   if (cu_seqlens == nullptr && num_tokens != num_seqs) return NDL_ERR_INVALID_ARG;
-  if (q_tok_stride < (int64_t)num_heads * head_dim ||
+  if ((q != nullptr && q_tok_stride < (int64_t)num_heads * head_dim) ||
       k_tok_stride < (int64_t)num_kv_heads * head_dim ||
       v_tok_stride < (int64_t)num_kv_heads * head_dim || cs_tok_stride < head_dim)
     return NDL_ERR_INVALID_ARG;
@@ -198,7 +198,8 @@ extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stri
   a.num_tokens = num_tokens;
   // one wave per (token, round of 64 items), 4 per workgroup
   const int64_t cph = head_dim / 16;
-  const int64_t rounds = (2 * num_kv_heads * cph + 63) / 64 + (num_heads * cph + 63) / 64;
+  const int64_t rounds = (2 * num_kv_heads * cph + 63) / 64 +
+                         (q != nullptr ? (num_heads * cph + 63) / 64 : 0);
   const int64_t blocks = (num_tokens * rounds + 3) / 4;
   if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
   hipLaunchKernelGGL(rope_kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0,

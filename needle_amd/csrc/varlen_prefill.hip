@@ -78,6 +78,10 @@ struct PrefillArgs {
   int64_t num_tokens;
   int num_seqs;
   int persistent;     // 1: grid of resident workgroups walking the tile list
+  // Rotary embedding of q (ROPE kernels): cos/sin rows of every packed token.
+  const u16* rope_cos;
+  const u16* rope_sin;
+  int64_t rope_stride;
 };
 
 // One workgroup tile, looked up one tile ahead by the persistent walk: jobs
@@ -173,7 +177,9 @@ __device__ __forceinline__ float half_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-template <int D, int NS>
+// ROPE: q is the raw projection; each Q row is rotated as it is read into the operand
+// registers (with the reference's bf16 rounding, rope8), from cos/sin rows of its token.
+template <int D, int NS, bool ROPE>
 __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(PrefillArgs a) {
   constexpr int KS = D / 16;          // k-steps of the QK MFMA (16 head_dim each)
   constexpr int DT = D / 32;          // 32-wide head_dim tiles of O^T
@@ -634,14 +640,44 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
         lds_dma16(qbase, (uint32_t)((rr * a.q_tok_stride + 8 * c) * 2), ql + 1024 * e);
       }
     }
+    // Rotary embedding operands: lane l holds chunks 2s + h (s < KS) of its row, and chunk
+    // c pairs with chunk c + D/16 (the other half of the row), which is chunk 2(s + KS/2) + h:
+    // the lane holds both halves of every pair, so the rotation needs no exchange.  cos/sin
+    // of the same chunks come straight from the token's rows (a row past the range reads the
+    // tile's first row; its Q operand is zeroed after the rotation).
+    u32x4 rcos[ROPE ? KS : 1], rsin[ROPE ? KS : 1];
+    if constexpr (ROPE) {
+      const int l = fresh_lane();   // offsets computed here, not hoisted out of the tile loop
+      const int rr = wave_active && wrow0 + (l & 31) < n ? wrow0 + (l & 31) : 0;
+      const int64_t off = (tok0 + rr) * a.rope_stride + 8 * (l >> 5);
+      const u16* cb = a.rope_cos + off;
+      const u16* sb = a.rope_sin + off;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        rcos[s] = ld16(cb + 16 * s);
+        rsin[s] = ld16(sb + 16 * s);
+      }
+    }
     ahead();
     vm_wait<0>();   // this wave's Q rows, and steps 0 and 1, landed
     {
       const bool ok = wave_active && wrow0 + r32 < n;
+      if constexpr (ROPE) {
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const u32x4 w = *reinterpret_cast<const u32x4*>(&qplane[koff[s]]);
-        qb[s] = __builtin_bit_cast(bf16x8, ok ? w : u32x4{0u, 0u, 0u, 0u});
+        for (int s = 0; s < KS / 2; ++s) {
+          const u32x4 lo = *reinterpret_cast<const u32x4*>(&qplane[koff[s]]);
+          const u32x4 hi = *reinterpret_cast<const u32x4*>(&qplane[koff[s + KS / 2]]);
+          u32x4 rlo, rhi;
+          rope8(lo, hi, rcos[s], rcos[s + KS / 2], rsin[s], rsin[s + KS / 2], rlo, rhi);
+          qb[s] = __builtin_bit_cast(bf16x8, ok ? rlo : u32x4{0u, 0u, 0u, 0u});
+          qb[s + KS / 2] = __builtin_bit_cast(bf16x8, ok ? rhi : u32x4{0u, 0u, 0u, 0u});
+        }
+      } else {
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(&qplane[koff[s]]);
+          qb[s] = __builtin_bit_cast(bf16x8, ok ? w : u32x4{0u, 0u, 0u, 0u});
+        }
       }
     }
     lds_barrier();
@@ -966,15 +1002,17 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
 
 }  // namespace ndl
 
-extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
-                                  const void* kv_cache, int64_t num_blocks,
-                                  const int32_t* block_table, int64_t bt_row_stride,
-                                  int max_blocks_per_seq, const int32_t* cu_seqlens,
-                                  const int32_t* context_lens, int num_seqs, int64_t num_tokens,
-                                  int max_seqlen, int max_context_len, int num_heads,
-                                  int num_kv_heads, int head_dim, int block_size, int dtype,
-                                  float scale, ndl_stream_t stream) {
-  using namespace ndl;
+namespace ndl {
+
+// Shared by both entry points; cos == nullptr: q is already rotated.
+static int launch_prefill(void* out, const void* q, int64_t q_tok_stride, const void* cos,
+                          const void* sin, int64_t cs_tok_stride, const void* kv_cache,
+                          int64_t num_blocks, const int32_t* block_table, int64_t bt_row_stride,
+                          int max_blocks_per_seq, const int32_t* cu_seqlens,
+                          const int32_t* context_lens, int num_seqs, int64_t num_tokens,
+                          int max_seqlen, int max_context_len, int num_heads, int num_kv_heads,
+                          int head_dim, int block_size, int dtype, float scale,
+                          ndl_stream_t stream) {
   if (dtype != NDL_DTYPE_BF16) return NDL_ERR_UNSUPPORTED;
   if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -982,6 +1020,10 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
   if (num_seqs < 0 || num_tokens < 0 || max_seqlen < 0 || max_context_len < 0 ||
       num_blocks <= 0 || max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq ||
       q_tok_stride < (int64_t)num_heads * head_dim)
+    return NDL_ERR_INVALID_ARG;
+  const bool rope = cos != nullptr || sin != nullptr;
+  if (rope && (cos == nullptr || sin == nullptr || cs_tok_stride < head_dim ||
+               (cs_tok_stride & 7) || (((uintptr_t)cos | (uintptr_t)sin) & 15u)))
     return NDL_ERR_INVALID_ARG;
   if (num_seqs == 0 || num_tokens == 0 || max_seqlen == 0) return NDL_OK;
   if (!out || !q || !kv_cache || !block_table || !cu_seqlens || !context_lens)
@@ -1018,6 +1060,9 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
   a.scale_log2 = scale * kLog2e;
   a.num_qtiles = (int)qtiles;
   a.num_tokens = num_tokens;
+  a.rope_cos = (const u16*)cos;
+  a.rope_sin = (const u16*)sin;
+  a.rope_stride = cs_tok_stride;
 
   hipStream_t s = (hipStream_t)stream;
   // Persistent launch (one resident workgroup per slot, walking the longest-first tile
@@ -1025,8 +1070,11 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
   a.num_seqs = num_seqs;
   a.persistent = num_seqs <= kPrefListSeqs && qtiles <= kPrefListLevels &&
                  gx * (int64_t)num_seqs * qtiles < ((int64_t)1 << 31);
-  const void* fn = head_dim == 128 ? (const void*)varlen_prefill_kernel<128, 6>
-                                   : (const void*)varlen_prefill_kernel<64, 8>;
+  const void* fn = head_dim == 128
+                       ? (rope ? (const void*)varlen_prefill_kernel<128, 6, true>
+                               : (const void*)varlen_prefill_kernel<128, 6, false>)
+                       : (rope ? (const void*)varlen_prefill_kernel<64, 8, true>
+                               : (const void*)varlen_prefill_kernel<64, 8, false>);
   dim3 grid((unsigned)gx, (unsigned)num_seqs, (unsigned)qtiles);
   if (a.persistent) {
     const int64_t slots = resident_workgroups(fn, 64 * waves);
@@ -1034,9 +1082,45 @@ extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride
     const int64_t items = gx * (int64_t)num_seqs * qtiles;   // upper bound of the list
     grid = dim3((unsigned)(items < slots ? items : slots), 1, 1);
   }
-  if (head_dim == 128)
-    hipLaunchKernelGGL((varlen_prefill_kernel<128, 6>), grid, dim3(64 * waves), 0, s, a);
-  else
-    hipLaunchKernelGGL((varlen_prefill_kernel<64, 8>), grid, dim3(64 * waves), 0, s, a);
+  void* args[] = {&a};
+  if (hipLaunchKernel(fn, grid, dim3(64 * waves), args, 0, s) != hipSuccess) {
+    (void)hipGetLastError();  // clear the error so that the next call's check sees its own
+    return NDL_ERR_LAUNCH;
+  }
   return check_launch();
+}
+
+}  // namespace ndl
+
+extern "C" int ndl_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
+                                  const void* kv_cache, int64_t num_blocks,
+                                  const int32_t* block_table, int64_t bt_row_stride,
+                                  int max_blocks_per_seq, const int32_t* cu_seqlens,
+                                  const int32_t* context_lens, int num_seqs, int64_t num_tokens,
+                                  int max_seqlen, int max_context_len, int num_heads,
+                                  int num_kv_heads, int head_dim, int block_size, int dtype,
+                                  float scale, ndl_stream_t stream) {
+  return ndl::launch_prefill(out, q, q_tok_stride, nullptr, nullptr, 0, kv_cache, num_blocks,
+                             block_table, bt_row_stride, max_blocks_per_seq, cu_seqlens,
+                             context_lens, num_seqs, num_tokens, max_seqlen, max_context_len,
+                             num_heads, num_kv_heads, head_dim, block_size, dtype, scale,
+                             stream);
+}
+
+extern "C" int ndl_rope_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
+                                       const void* cos, const void* sin, int64_t cs_tok_stride,
+                                       const void* kv_cache, int64_t num_blocks,
+                                       const int32_t* block_table, int64_t bt_row_stride,
+                                       int max_blocks_per_seq, const int32_t* cu_seqlens,
+                                       const int32_t* context_lens, int num_seqs,
+                                       int64_t num_tokens, int max_seqlen, int max_context_len,
+                                       int num_heads, int num_kv_heads, int head_dim,
+                                       int block_size, int dtype, float scale,
+                                       ndl_stream_t stream) {
+  if (cos == nullptr || sin == nullptr) return NDL_ERR_INVALID_ARG;
+  return ndl::launch_prefill(out, q, q_tok_stride, cos, sin, cs_tok_stride, kv_cache,
+                             num_blocks, block_table, bt_row_stride, max_blocks_per_seq,
+                             cu_seqlens, context_lens, num_seqs, num_tokens, max_seqlen,
+                             max_context_len, num_heads, num_kv_heads, head_dim, block_size,
+                             dtype, scale, stream);
 }

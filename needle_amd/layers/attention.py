@@ -7,8 +7,9 @@ head_dim].  Projections stay torch GEMMs (attention.py:84-86).  The rest of
 forward is, bit-exact with the reference's bf16 rounding of RoPE (attention.py:88,
 277-288):
 
-  prefill (attention.py:88, 102-107): ndl_rope_kv_append (RoPE of q and k, the append of
-          k and v), then ndl_varlen_prefill
+  prefill (attention.py:88, 102-107): ndl_rope_kv_append with q = NULL (RoPE of k, the
+          append of k and v), then ndl_rope_varlen_prefill, which rotates each query row
+          as it reads q: no rotated q is written or read back
   decode  (attention.py:88, 140-159): ndl_rope_paged_decode_append, one launch for RoPE,
           the append and the attention (plus the merge launch of the stream split)
 
@@ -85,10 +86,10 @@ class Attention(nn.Module):
         v = self.v_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
         if self.fuse_rope:
             if is_prefill:
-                q = ops.rope_kv_append(q, k, v, cos, sin, kv_cache, block_table, context_lens,
-                                       cu_seqlens)
+                ops.rope_kv_append(None, k, v, cos, sin, kv_cache, block_table, context_lens,
+                                   cu_seqlens)
                 out = self._prefill_attend(q, kv_cache, block_table, cu_seqlens, context_lens,
-                                           max_seqlen)
+                                           max_seqlen, cos=cos, sin=sin)
             else:
                 out = self._decode_attend(q, kv_cache, block_table, context_lens, new_k=k,
                                           new_v=v, cos=cos, sin=sin)
@@ -106,10 +107,12 @@ class Attention(nn.Module):
         return self._prefill_attend(q, kv_cache, block_table, cu_seqlens, context_lens,
                                     max_seqlen)
 
-    def _prefill_attend(self, q, kv_cache, block_table, cu_seqlens, context_lens, max_seqlen):
+    def _prefill_attend(self, q, kv_cache, block_table, cu_seqlens, context_lens, max_seqlen,
+                        cos=None, sin=None):
+        """Prefill attention; with cos/sin, q is the raw projection, rotated in the kernel."""
         return ops.varlen_prefill(q, kv_cache, block_table, cu_seqlens, context_lens,
                                   int(max_seqlen), self.scale, self.num_heads,
-                                  self.num_kv_heads, self.head_dim)
+                                  self.num_kv_heads, self.head_dim, cos=cos, sin=sin)
 
     def _decode(self, q, k, v, kv_cache, block_table, context_lens):
         return self._decode_attend(q, kv_cache, block_table, context_lens, new_k=k, new_v=v)

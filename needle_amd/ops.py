@@ -115,30 +115,39 @@ def kv_append(k: torch.Tensor, v: torch.Tensor, kv_cache: torch.Tensor,
     _lib.check(rc, "ndl_kv_append")
 
 
-def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch.Tensor,
-                   sin: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
-                   context_lens: torch.Tensor, cu_seqlens: Optional[torch.Tensor] = None,
-                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+def rope_kv_append(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor,
+                   cos: torch.Tensor, sin: torch.Tensor, kv_cache: torch.Tensor,
+                   block_table: torch.Tensor, context_lens: torch.Tensor,
+                   cu_seqlens: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None) -> Optional[torch.Tensor]:
     """Rotate q/k by (cos, sin) and append rotated k and v to kv_cache; returns rotated q.
 
     Same result as _apply_rope (attention.py:88, :277-288) followed by the append
     of attention.py:141-154 (cu_seqlens=None) or _write_kv (:204-246), bit for bit.
     q [T, H, D], k/v [T, Hkv, D], cos/sin [T, D] in the cache dtype (bf16).
+    q=None rotates and appends k (and appends v) only, and returns None: the form that
+    precedes rope_varlen_prefill, which rotates q itself.
     """
     _check_cache(kv_cache)
     dev = kv_cache.device
     _, num_blocks, hkv, bs, d = kv_cache.shape
     _require(kv_cache.dtype == torch.bfloat16, "rope_kv_append supports bfloat16 only", TypeError)
     for name, x in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
-        _require(x.dtype == kv_cache.dtype, f"{name} dtype must match kv_cache", TypeError)
-    _require(q.dim() == 3, f"q must be [T, H, {d}], got {tuple(q.shape)}")
-    h = q.shape[1]
-    qs = _rows("q", q, h, d, dev)
+        _require(x is None or x.dtype == kv_cache.dtype, f"{name} dtype must match kv_cache",
+                 TypeError)
     ks = _rows("k", k, hkv, d, dev)
     vs = _rows("v", v, hkv, d, dev)
-    n_tok = q.shape[0]
-    _require(k.shape[0] == n_tok and v.shape[0] == n_tok, "q/k/v token counts differ")
-    _require(h % hkv == 0, f"num_heads {h} not a multiple of num_kv_heads {hkv}")
+    n_tok = k.shape[0]
+    if q is not None:
+        _require(q.dim() == 3, f"q must be [T, H, {d}], got {tuple(q.shape)}")
+        h = q.shape[1]
+        qs = _rows("q", q, h, d, dev)
+        _require(q.shape[0] == n_tok, "q/k/v token counts differ")
+        _require(h % hkv == 0, f"num_heads {h} not a multiple of num_kv_heads {hkv}")
+    else:
+        _require(out is None, "out is the rotated q: pass q with it")
+        h, qs = hkv, 0
+    _require(v.shape[0] == n_tok, "q/k/v token counts differ")
     _require(d % 16 == 0, f"head_dim {d} must be a multiple of 16")
     for name, x in (("cos", cos), ("sin", sin)):
         _require(x.dim() == 2 and x.shape[0] == n_tok and x.shape[1] == d,
@@ -156,7 +165,9 @@ def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch
     else:
         _check_int32("cu_seqlens", cu_seqlens, 1, dev)
         _require(cu_seqlens.shape[0] == n_seqs + 1, "cu_seqlens must be [num_seqs + 1]")
-    if out is None:
+    if q is None:
+        pass
+    elif out is None:
         out = torch.empty((n_tok, h, d), dtype=q.dtype, device=dev)
     else:
         _require(out.shape == (n_tok, h, d) and out.is_contiguous() and out.dtype == q.dtype
@@ -168,7 +179,7 @@ def rope_kv_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cos: torch
         _validate_slots(block_table, num_blocks)
     lib = _lib.load()
     rc = lib.ndl_rope_kv_append(
-        out.data_ptr(), q.data_ptr(), qs, k.data_ptr(), ks, v.data_ptr(), vs,
+        _ptr(out), _ptr(q), qs, k.data_ptr(), ks, v.data_ptr(), vs,
         cos.data_ptr(), sin.data_ptr(), cs,
         kv_cache.data_ptr(), num_blocks, h, hkv, bs, d, _DTYPES[kv_cache.dtype],
         block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
@@ -296,13 +307,18 @@ def decode_workspace(nbytes: int, device) -> torch.Tensor:
 def varlen_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.Tensor,
                    cu_seqlens: torch.Tensor, context_lens: torch.Tensor, max_seqlen: int,
                    scale: float, num_heads: int, num_kv_heads: int, head_dim: int, *,
-                   max_context_len: int = 0,
-                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                   max_context_len: int = 0, out: Optional[torch.Tensor] = None,
+                   cos: Optional[torch.Tensor] = None,
+                   sin: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Causal attention of packed prompts over the paged cache (after kv_append).
 
     Equals the reference _prefill_pytorch (attention.py:120-134) when every
     context_lens entry is 0; with a cached prefix the prefix is attended too.
     Returns [num_tokens, num_heads, head_dim].
+    With cos/sin ([T, D] rows of the packed tokens), q is the raw projection and each row
+    is rotated inside the kernel (ndl_rope_varlen_prefill): the output is bit-identical to
+    rope_kv_append's rotated q fed to this function, with k already rotated in the cache
+    (rope_kv_append with q=None).
     """
     _check_cache(kv_cache)
     dev = kv_cache.device
@@ -317,6 +333,17 @@ def varlen_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.T
     _require(cu_seqlens.shape[0] == n_seqs + 1 and context_lens.shape[0] == n_seqs,
              "cu_seqlens / context_lens / block_table batch mismatch")
     n_tok = q.shape[0]
+    _require((cos is None) == (sin is None), "pass both cos and sin, or neither")
+    cs = 0
+    if cos is not None:
+        for name, x in (("cos", cos), ("sin", sin)):
+            _require(x.dtype == q.dtype, f"{name} dtype must match q", TypeError)
+            _require(x.dim() == 2 and x.shape[0] == n_tok and x.shape[1] == head_dim,
+                     f"{name} must be [{n_tok}, {head_dim}], got {tuple(x.shape)}")
+            _require(x.device == dev and x.stride(1) == 1,
+                     f"{name} rows must be contiguous on {dev}")
+        _require(cos.stride(0) == sin.stride(0) or n_tok <= 1, "cos and sin token strides differ")
+        cs = cos.stride(0) if n_tok > 1 else head_dim
     if out is None:
         out = torch.empty((n_tok, num_heads, head_dim), dtype=q.dtype, device=dev)
     else:
@@ -330,13 +357,18 @@ def varlen_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.T
     if _validate_enabled():
         _validate_slots(block_table, num_blocks)
     lib = _lib.load()
-    rc = lib.ndl_varlen_prefill(
-        out.data_ptr(), q.data_ptr(), qs, kv_cache.data_ptr(), num_blocks,
-        block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
-        cu_seqlens.data_ptr(), context_lens.data_ptr(), n_seqs, n_tok, int(max_seqlen),
-        int(max_context_len), num_heads, num_kv_heads, head_dim, bs, _DTYPES[q.dtype],
-        float(scale), _stream(dev))
-    _lib.check(rc, "ndl_varlen_prefill")
+    tail = (kv_cache.data_ptr(), num_blocks,
+            block_table.data_ptr(), block_table.stride(0), block_table.shape[1],
+            cu_seqlens.data_ptr(), context_lens.data_ptr(), n_seqs, n_tok, int(max_seqlen),
+            int(max_context_len), num_heads, num_kv_heads, head_dim, bs, _DTYPES[q.dtype],
+            float(scale), _stream(dev))
+    if cos is None:
+        rc = lib.ndl_varlen_prefill(out.data_ptr(), q.data_ptr(), qs, *tail)
+        _lib.check(rc, "ndl_varlen_prefill")
+    else:
+        rc = lib.ndl_rope_varlen_prefill(out.data_ptr(), q.data_ptr(), qs, cos.data_ptr(),
+                                         sin.data_ptr(), cs, *tail)
+        _lib.check(rc, "ndl_rope_varlen_prefill")
     return out
 
 

@@ -39,7 +39,7 @@ def test_every_declared_symbol_is_exported(lib):
 def test_version_and_status_text(lib):
     assert lib.ndl_abi_version() == _lib.NDL_ABI_VERSION
     assert lib.ndl_strerror(0) == b"ok"
-    for code in (-1, -2, -3, -4, -5):
+    for code in (-1, -2, -3, -4, -5, -6):
         assert lib.ndl_strerror(code) and lib.ndl_strerror(code) != b"unknown status"
     assert lib.ndl_strerror(-99) == b"unknown status"
 
@@ -98,6 +98,15 @@ def test_rejections_before_any_launch(lib):
     assert rope(d=72) == -2
     assert rope(t=0) == 0
     assert rope() == -1
+    # rope_varlen_prefill: cos/sin are required (the plain entry point takes none); an
+    # unsupported dtype is refused before any launch
+    def rope_prefill(cos=None, dtype=0, cs=128):
+        return lib.ndl_rope_varlen_prefill(None, None, 4 * 128, cos, cos, cs, None, 1, None, 1,
+                                           1, None, None, 1, 1, 1, 0, 4, 1, 128, 16, dtype, 1.0,
+                                           None)
+    assert rope_prefill() == -1
+    assert rope_prefill(cos=1 << 20, dtype=1) == -2
+    assert rope_prefill(cos=1 << 20, cs=100) == -1
     # the allocation-free decode: a shape whose partials exceed the static array is refused
     # after the argument checks and before any device call (1000 sequences x 1000 blocks at
     # 16 tokens per wave); the aligned stand-in addresses are never dereferenced

@@ -34,7 +34,7 @@ def test_prefill_kernels_use_m0_only_for_direct_lds_loads(tmp_path):
     lines = asm.read_text().splitlines()
     kernels = [i for i, l in enumerate(lines)
                if re.match(r"_ZN3ndl21varlen_prefill_kernel.*:", l)]
-    assert len(kernels) == 2
+    assert len(kernels) == 4          # head_dim 64 and 128, each with and without RoPE of q
     for start in kernels:
         end = next(i for i in range(start, len(lines)) if lines[i].startswith(".Lfunc_end"))
         body = [l.strip() for l in lines[start:end] if not l.strip().startswith(";")]
