@@ -43,7 +43,11 @@ constexpr int kAppendSmallSeqs = 63;
 // TPW is a template argument so that every wave issues the same loads and the compiler's
 // vector-memory waits count them exactly; the last wave reloads its last valid token's
 // row for the tokens past the end and stores nothing for them.
-template <int TPW, bool SMALL>
+// ROPE: k is rotated on the way (the rotary embedding of ndl_rope_kv_append, rope8, from
+// the token's cos/sin rows).  A lane then moves a chunk pair (c, c + head_dim/16) of one
+// row, the rotation's operands: items are the k rows' pairs, then the v rows' pairs (copied
+// unrotated), the same count as the chunks of one plane without ROPE.
+template <int TPW, bool SMALL, bool ROPE>
 __global__ __launch_bounds__(256) void kv_append_kernel(
     u16* __restrict__ cache, int64_t plane_elems, int64_t num_blocks, int num_kv_heads,
     int block_size, int head_dim,
@@ -51,7 +55,8 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
     const u16* __restrict__ v, int64_t v_tok_stride,
     const int32_t* __restrict__ block_table, int64_t bt_row_stride, int max_blocks,
     const int32_t* __restrict__ cu_seqlens, const int32_t* __restrict__ context_lens,
-    int num_seqs, int64_t num_tokens) {
+    int num_seqs, int64_t num_tokens, const u16* __restrict__ rope_cos,
+    const u16* __restrict__ rope_sin, int64_t rope_stride) {
   const int lane = threadIdx.x & 63;
   const int64_t wave_id =
       (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
@@ -130,8 +135,99 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
       }
     }
   };
-  round(0, true);  // outside the loop: straight-line code, no waits between its loads
-  for (int r = 1; r < (cpt + 63) / 64; ++r) round(r, false);
+  // ROPE rounds: item cc < cpt/2 is pair c of k row h, the rest the same pairs of v.
+  const int half = cpr >> 1, pairs = cpt >> 1;
+  auto rope_round = [&](const int r, const bool first) {
+    const int cc0 = r * 64 + lane;
+    const bool live = cc0 < cpt;
+    const int cc = live ? cc0 : cpt - 1;
+    const bool is_v = cc >= pairs;
+    const int pi = is_v ? cc - pairs : cc;
+    const int h = pi / half, c = pi - h * half;
+    const u16* const src = is_v ? v : k;
+    const int64_t src_stride = is_v ? v_tok_stride : k_tok_stride;
+    const int64_t in_off = (int64_t)h * head_dim + c * 8;
+    u32x4 xl[TPW], xh[TPW], cl[TPW], ch[TPW], sl[TPW], sh[TPW];
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      const int64_t t = t0 + u < num_tokens ? t0 + u : t_last;
+      const u16* const x = src + t * src_stride + in_off;
+      const u16* const cs = rope_cos + t * rope_stride + c * 8;
+      const u16* const sn = rope_sin + t * rope_stride + c * 8;
+      xl[u] = ld16(x);
+      xh[u] = ld16(x + half * 8);
+      cl[u] = ld16(cs);
+      ch[u] = ld16(cs + half * 8);
+      sl[u] = ld16(sn);
+      sh[u] = ld16(sn + half * 8);
+    }
+    if (first) lookup();
+    u16* const plane = cache + (is_v ? plane_elems : 0);
+    const int64_t out_off = ((int64_t)h * block_size) * head_dim + c * 8;
+#pragma unroll
+    for (int u = 0; u < TPW; ++u) {
+      u32x4 ol = xl[u], oh = xh[u];
+      if (!is_v) rope8(xl[u], xh[u], cl[u], ch[u], sl[u], sh[u], ol, oh);
+      if (live && dst_row[u] >= 0) {
+        st16(plane + dst_row[u] + out_off, ol);
+        st16(plane + dst_row[u] + out_off + half * 8, oh);
+      }
+    }
+  };
+  if constexpr (ROPE) {
+    rope_round(0, true);
+    for (int r = 1; r < (cpt + 63) / 64; ++r) rope_round(r, false);
+  } else {
+    round(0, true);  // outside the loop: straight-line code, no waits between its loads
+    for (int r = 1; r < (cpt + 63) / 64; ++r) round(r, false);
+  }
+}
+
+// Shared by ndl_kv_append and the k-only form of ndl_rope_kv_append (rope_cos != nullptr:
+// k rotated; head_dim a multiple of 16).  Arguments are checked by the callers.
+int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int block_size,
+                     int head_dim, const void* k, int64_t k_tok_stride, const void* v,
+                     int64_t v_tok_stride, const int32_t* block_table, int64_t bt_row_stride,
+                     int max_blocks_per_seq, const int32_t* cu_seqlens,
+                     const int32_t* context_lens, int num_seqs, int64_t num_tokens,
+                     const void* rope_cos, const void* rope_sin, int64_t rope_stride,
+                     ndl_stream_t stream) {
+  const int64_t plane_elems = num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
+  const bool small = cu_seqlens != nullptr && num_seqs <= kAppendSmallSeqs;
+  const bool rope = rope_cos != nullptr;
+  // As few tokens per wave as keep every wave resident at once (a second, partial round
+  // of waves costs more than longer waves: 17,705 tokens of 4 x 128 went 13.3 us at 1
+  // or 2 tokens per wave, 12.9 us at 3, 14.1 us at 4 on MI355X).
+  int64_t resident = resident_workgroups((const void*)kv_append_kernel<1, false, false>, 256) * 4;
+  if (resident <= 0) resident = 8192;
+  int64_t tpw64 = (num_tokens + resident - 1) / resident;
+  const int tpw = (int)(tpw64 < 1 ? 1 : tpw64 > kAppendMaxTokensPerWave ? kAppendMaxTokensPerWave
+                                                                        : tpw64);
+  const int64_t waves = (num_tokens + tpw - 1) / tpw;
+  const int64_t blocks = (waves + 3) / 4;
+  if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
+#define NDL_APPEND_FNS(S, R)                                                          \
+  {(const void*)kv_append_kernel<1, S, R>, (const void*)kv_append_kernel<2, S, R>,    \
+   (const void*)kv_append_kernel<3, S, R>, (const void*)kv_append_kernel<4, S, R>}
+  const void* fns[2][2][kAppendMaxTokensPerWave] = {
+      {NDL_APPEND_FNS(false, false), NDL_APPEND_FNS(true, false)},
+      {NDL_APPEND_FNS(false, true), NDL_APPEND_FNS(true, true)}};
+#undef NDL_APPEND_FNS
+  u16* cache = (u16*)kv_cache;
+  const u16* kp = (const u16*)k;
+  const u16* vp = (const u16*)v;
+  const u16* cp = (const u16*)rope_cos;
+  const u16* sp = (const u16*)rope_sin;
+  void* args[] = {&cache, (void*)&plane_elems, &num_blocks, &num_kv_heads, &block_size,
+                  &head_dim, &kp, &k_tok_stride, &vp, &v_tok_stride, &block_table,
+                  &bt_row_stride, &max_blocks_per_seq, &cu_seqlens, &context_lens, &num_seqs,
+                  &num_tokens, &cp, &sp, &rope_stride};
+  if (hipLaunchKernel(fns[rope ? 1 : 0][small ? 1 : 0][tpw - 1], dim3((unsigned)blocks),
+                      dim3(256), args, 0, (hipStream_t)stream) != hipSuccess) {
+    (void)hipGetLastError();  // clear the error so that the next call's check sees its own
+    return NDL_ERR_LAUNCH;
+  }
+  return check_launch();
 }
 
 }  // namespace ndl
@@ -161,35 +257,8 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
   if (((uintptr_t)kv_cache | (uintptr_t)k | (uintptr_t)v) & 15u) return NDL_ERR_INVALID_ARG;
   if ((k_tok_stride | v_tok_stride) & 7) return NDL_ERR_INVALID_ARG;
 
-  const int64_t plane_elems = num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
-  const bool small = cu_seqlens != nullptr && num_seqs <= kAppendSmallSeqs;
-  // As few tokens per wave as keep every wave resident at once (a second, partial round
-  // of waves costs more than longer waves: 17,705 tokens of 4 x 128 went 13.3 us at 1
-  // or 2 tokens per wave, 12.9 us at 3, 14.1 us at 4 on MI355X).
-  int64_t resident = resident_workgroups((const void*)kv_append_kernel<1, false>, 256) * 4;
-  if (resident <= 0) resident = 8192;
-  int64_t tpw64 = (num_tokens + resident - 1) / resident;
-  const int tpw = (int)(tpw64 < 1 ? 1 : tpw64 > kAppendMaxTokensPerWave ? kAppendMaxTokensPerWave
-                                                                        : tpw64);
-  const int64_t waves = (num_tokens + tpw - 1) / tpw;
-  const int64_t blocks = (waves + 3) / 4;
-  if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
-  const void* fns[2][kAppendMaxTokensPerWave] = {
-      {(const void*)kv_append_kernel<1, false>, (const void*)kv_append_kernel<2, false>,
-       (const void*)kv_append_kernel<3, false>, (const void*)kv_append_kernel<4, false>},
-      {(const void*)kv_append_kernel<1, true>, (const void*)kv_append_kernel<2, true>,
-       (const void*)kv_append_kernel<3, true>, (const void*)kv_append_kernel<4, true>}};
-  u16* cache = (u16*)kv_cache;
-  const u16* kp = (const u16*)k;
-  const u16* vp = (const u16*)v;
-  void* args[] = {&cache, (void*)&plane_elems, &num_blocks, &num_kv_heads, &block_size,
-                  &head_dim, &kp, &k_tok_stride, &vp, &v_tok_stride, &block_table,
-                  &bt_row_stride, &max_blocks_per_seq, &cu_seqlens, &context_lens, &num_seqs,
-                  &num_tokens};
-  if (hipLaunchKernel(fns[small ? 1 : 0][tpw - 1], dim3((unsigned)blocks), dim3(256), args, 0,
-                      (hipStream_t)stream) != hipSuccess) {
-    (void)hipGetLastError();  // clear the error so that the next call's check sees its own
-    return NDL_ERR_LAUNCH;
-  }
-  return check_launch();
+  return launch_kv_append(kv_cache, num_blocks, num_kv_heads, block_size, head_dim, k,
+                          k_tok_stride, v, v_tok_stride, block_table, bt_row_stride,
+                          max_blocks_per_seq, cu_seqlens, context_lens, num_seqs, num_tokens,
+                          nullptr, nullptr, 0, stream);
 }

@@ -48,31 +48,23 @@ __device__ __forceinline__ uint32_t pack_halves(uint32_t lo, uint32_t hi, bool h
 //   rot(x)[d] = -x[d + D/2] (d < D/2), x[d - D/2] (d >= D/2);
 // every product and the sum are formed in fp32 from bf16 operands and rounded to nearest
 // even, as torch does for bf16 tensors.
-__device__ __forceinline__ float round_bf16(float x) {
-  return __uint_as_float(f32_to_bf16_bits(x) << 16);
-}
-
-// 8 bf16 of x[d..d+8) and x[d+D/2..d+D/2+8) -> rotated halves.
+// 8 bf16 of x[d..d+8) and x[d+D/2..d+D/2+8) -> rotated halves.  The two elements of a
+// word are rounded together (one v_cvt_pk_bf16_f32 per pair of products, each half rounded
+// to nearest even on its own, exactly as two single roundings).
 __device__ __forceinline__ void rope8(const u32x4& lo, const u32x4& hi, const u32x4& clo,
                                       const u32x4& chi, const u32x4& slo, const u32x4& shi,
                                       u32x4& out_lo, u32x4& out_hi) {
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    float a[2], b[2];
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const float xl = h ? bf16_hi(lo[w]) : bf16_lo(lo[w]);
-      const float xh = h ? bf16_hi(hi[w]) : bf16_lo(hi[w]);
-      const float cl = h ? bf16_hi(clo[w]) : bf16_lo(clo[w]);
-      const float ch = h ? bf16_hi(chi[w]) : bf16_lo(chi[w]);
-      const float sl = h ? bf16_hi(slo[w]) : bf16_lo(slo[w]);
-      const float sh = h ? bf16_hi(shi[w]) : bf16_lo(shi[w]);
-      // first half: x*cos + (-x_hi)*sin ; second half: x_hi*cos + x*sin
-      a[h] = round_bf16(xl * cl) + round_bf16(-xh * sl);
-      b[h] = round_bf16(xh * ch) + round_bf16(xl * sh);
-    }
-    out_lo[w] = pack_bf16x2(a[0], a[1]);
-    out_hi[w] = pack_bf16x2(b[0], b[1]);
+    const float xl0 = bf16_lo(lo[w]), xl1 = bf16_hi(lo[w]);
+    const float xh0 = bf16_lo(hi[w]), xh1 = bf16_hi(hi[w]);
+    // first half: x*cos + (-x_hi)*sin ; second half: x_hi*cos + x*sin
+    const uint32_t p_xc = pack_bf16x2(xl0 * bf16_lo(clo[w]), xl1 * bf16_hi(clo[w]));
+    const uint32_t p_rs = pack_bf16x2(-xh0 * bf16_lo(slo[w]), -xh1 * bf16_hi(slo[w]));
+    const uint32_t p_hc = pack_bf16x2(xh0 * bf16_lo(chi[w]), xh1 * bf16_hi(chi[w]));
+    const uint32_t p_ls = pack_bf16x2(xl0 * bf16_lo(shi[w]), xl1 * bf16_hi(shi[w]));
+    out_lo[w] = pack_bf16x2(bf16_lo(p_xc) + bf16_lo(p_rs), bf16_hi(p_xc) + bf16_hi(p_rs));
+    out_hi[w] = pack_bf16x2(bf16_lo(p_hc) + bf16_lo(p_ls), bf16_hi(p_hc) + bf16_hi(p_ls));
   }
 }
 
@@ -126,5 +118,14 @@ inline int64_t resident_workgroups(const void* fn, int block) {
   if (used < 64) cache[used++] = Entry{fn, block, dev, wgs};
   return wgs;
 }
+
+// The append launcher of kv_append.hip (rope_cos != nullptr: k rotated by rope8).
+int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int block_size,
+                     int head_dim, const void* k, int64_t k_tok_stride, const void* v,
+                     int64_t v_tok_stride, const int32_t* block_table, int64_t bt_row_stride,
+                     int max_blocks_per_seq, const int32_t* cu_seqlens,
+                     const int32_t* context_lens, int num_seqs, int64_t num_tokens,
+                     const void* rope_cos, const void* rope_sin, int64_t rope_stride,
+                     ndl_stream_t stream);
 
 }  // namespace ndl

@@ -89,7 +89,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
       (int64_t)blockIdx.x * 4 + __builtin_amdgcn_readfirstlane((int)(threadIdx.x >> 6));
   const int D = a.head_dim, half = D >> 1, cph = half >> 3;  // chunks per half row
   const int H = a.num_heads, Hkv = a.num_kv_heads, bs = a.block_size;
-  const int kv_items = 2 * Hkv * cph, q_items = a.q != nullptr ? H * cph : 0;
+  const int kv_items = 2 * Hkv * cph, q_items = H * cph;
   const int kv_rounds = (kv_items + 63) >> 6, rounds = kv_rounds + ((q_items + 63) >> 6);
   const int64_t t = w / rounds;
   const int r = (int)(w - t * rounds);
@@ -171,6 +171,11 @@ extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stri
     return NDL_ERR_INVALID_ARG;
   if ((q_tok_stride | k_tok_stride | v_tok_stride | cs_tok_stride) & 7) return NDL_ERR_INVALID_ARG;
 
+  if (q == nullptr)  // k rotated and k, v appended: the append kernel with the rotation
+    return launch_kv_append(kv_cache, num_blocks, num_kv_heads, block_size, head_dim, k,
+                            k_tok_stride, v, v_tok_stride, block_table, bt_row_stride,
+                            max_blocks_per_seq, cu_seqlens, context_lens, num_seqs, num_tokens,
+                            cos, sin, cs_tok_stride, stream);
   RopeArgs a;
   a.q_out = (u16*)q_out;
   a.q = (const u16*)q;
@@ -198,8 +203,7 @@ extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stri
   a.num_tokens = num_tokens;
   // one wave per (token, round of 64 items), 4 per workgroup
   const int64_t cph = head_dim / 16;
-  const int64_t rounds = (2 * num_kv_heads * cph + 63) / 64 +
-                         (q != nullptr ? (num_heads * cph + 63) / 64 : 0);
+  const int64_t rounds = (2 * num_kv_heads * cph + 63) / 64 + (num_heads * cph + 63) / 64;
   const int64_t blocks = (num_tokens * rounds + 3) / 4;
   if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
   hipLaunchKernelGGL(rope_kv_append_kernel, dim3((unsigned)blocks), dim3(256), 0,

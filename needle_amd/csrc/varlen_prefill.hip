@@ -640,44 +640,53 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
         lds_dma16(qbase, (uint32_t)((rr * a.q_tok_stride + 8 * c) * 2), ql + 1024 * e);
       }
     }
-    // Rotary embedding operands: lane l holds chunks 2s + h (s < KS) of its row, and chunk
-    // c pairs with chunk c + D/16 (the other half of the row), which is chunk 2(s + KS/2) + h:
-    // the lane holds both halves of every pair, so the rotation needs no exchange.  cos/sin
-    // of the same chunks come straight from the token's rows (a row past the range reads the
-    // tile's first row; its Q operand is zeroed after the rotation).
-    u32x4 rcos[ROPE ? KS : 1], rsin[ROPE ? KS : 1];
+    // Rotary embedding of the staged Q rows (ROPE).  Row r's element pairs (d, d + D/2) are
+    // chunk pairs (p, p + KS), KS = D/16 pairs per row; lane l takes pair l % KS of rows
+    // (64/KS) i + l / KS, i < KS/2, so that each cos/sin load instruction covers whole
+    // 128-byte halves of rows (coalesced).  Those loads go out with the Q rows; once both
+    // have landed the lane rotates its pairs in the wave's own Q plane (read, rope8, write
+    // back: the wave's LDS accesses complete in order), and the operand layout is read
+    // from the rotated rows below.  A row past the range reads the tile's first row of
+    // cos/sin; its Q operand is zeroed when read.
+    constexpr int RIPL = ROPE ? KS / 2 : 1;      // (row, pair) items per lane
+    u32x4 rcos[RIPL][2], rsin[RIPL][2];
     if constexpr (ROPE) {
       const int l = fresh_lane();   // offsets computed here, not hoisted out of the tile loop
-      const int rr = wave_active && wrow0 + (l & 31) < n ? wrow0 + (l & 31) : 0;
-      const int64_t off = (tok0 + rr) * a.rope_stride + 8 * (l >> 5);
-      const u16* cb = a.rope_cos + off;
-      const u16* sb = a.rope_sin + off;
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        rcos[s] = ld16(cb + 16 * s);
-        rsin[s] = ld16(sb + 16 * s);
+      for (int i = 0; i < RIPL; ++i) {
+        const int row = (64 / KS) * i + l / KS, p = l % KS;
+        const int rr = wave_active && wrow0 + row < n ? wrow0 + row : 0;
+        const int64_t off = (tok0 + rr) * a.rope_stride + 8 * p;
+        rcos[i][0] = ld16(a.rope_cos + off);
+        rcos[i][1] = ld16(a.rope_cos + off + D / 2);
+        rsin[i][0] = ld16(a.rope_sin + off);
+        rsin[i][1] = ld16(a.rope_sin + off + D / 2);
       }
     }
     ahead();
-    vm_wait<0>();   // this wave's Q rows, and steps 0 and 1, landed
+    vm_wait<0>();   // this wave's Q rows (and cos/sin), and steps 0 and 1, landed
+    if constexpr (ROPE) {
+      const int l = fresh_lane();
+#pragma unroll
+      for (int i = 0; i < RIPL; ++i) {
+        const int row = (64 / KS) * i + l / KS, p = l % KS;
+        u16* const lo_at = qplane + row * D + 8 * (p ^ pref_swz<D>(row));
+        u16* const hi_at = qplane + row * D + 8 * ((p + KS) ^ pref_swz<D>(row));
+        u32x4 lo = *reinterpret_cast<const u32x4*>(lo_at);
+        u32x4 hi = *reinterpret_cast<const u32x4*>(hi_at);
+        u32x4 rlo, rhi;
+        rope8(lo, hi, rcos[i][0], rcos[i][1], rsin[i][0], rsin[i][1], rlo, rhi);
+        *reinterpret_cast<u32x4*>(lo_at) = rlo;
+        *reinterpret_cast<u32x4*>(hi_at) = rhi;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
     {
       const bool ok = wave_active && wrow0 + r32 < n;
-      if constexpr (ROPE) {
 #pragma unroll
-        for (int s = 0; s < KS / 2; ++s) {
-          const u32x4 lo = *reinterpret_cast<const u32x4*>(&qplane[koff[s]]);
-          const u32x4 hi = *reinterpret_cast<const u32x4*>(&qplane[koff[s + KS / 2]]);
-          u32x4 rlo, rhi;
-          rope8(lo, hi, rcos[s], rcos[s + KS / 2], rsin[s], rsin[s + KS / 2], rlo, rhi);
-          qb[s] = __builtin_bit_cast(bf16x8, ok ? rlo : u32x4{0u, 0u, 0u, 0u});
-          qb[s + KS / 2] = __builtin_bit_cast(bf16x8, ok ? rhi : u32x4{0u, 0u, 0u, 0u});
-        }
-      } else {
-#pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(&qplane[koff[s]]);
-          qb[s] = __builtin_bit_cast(bf16x8, ok ? w : u32x4{0u, 0u, 0u, 0u});
-        }
+      for (int s = 0; s < KS; ++s) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(&qplane[koff[s]]);
+        qb[s] = __builtin_bit_cast(bf16x8, ok ? w : u32x4{0u, 0u, 0u, 0u});
       }
     }
     lds_barrier();

@@ -3,7 +3,9 @@
 The oracle applies RoPE as the reference does (attention.py:277-288, torch bf16
 ops) and then appends (attention.py:141-154 for decode, :204-246 for varlen).
 The fused launch must produce the same q bits and leave the same pool bits,
-including the random bit patterns outside the owned slots.
+including the random bit patterns outside the owned slots.  The k-only form (q = NULL,
+which the drop-in prefill uses before ndl_rope_varlen_prefill; it runs the append
+kernel's rotating variant) must leave the same pool bits too.
 """
 import pytest
 import torch
@@ -34,7 +36,7 @@ def _positions(case):
     return pos
 
 
-def _parity(case, base=1e6, q=None, k=None, v=None):
+def _parity(case, base=1e6, q=None, k=None, v=None, with_q=True):
     q = case.q if q is None else q
     k = case.k if k is None else k
     v = case.v if v is None else v
@@ -46,10 +48,13 @@ def _parity(case, base=1e6, q=None, k=None, v=None):
     else:
         paged_ref.write_kv(kr, v, want, case.block_table, case.cu_seqlens, case.context_lens)
     g = case.to(DEV)
-    qo = ops.rope_kv_append(q.to(DEV), k.to(DEV), v.to(DEV), cos.to(DEV), sin.to(DEV),
-                            g.kv_cache, g.block_table, g.context_lens, g.cu_seqlens)
+    qo = ops.rope_kv_append(q.to(DEV) if with_q else None, k.to(DEV), v.to(DEV), cos.to(DEV),
+                            sin.to(DEV), g.kv_cache, g.block_table, g.context_lens, g.cu_seqlens)
     torch.cuda.synchronize()
-    assert torch.equal(_bits(qo.cpu()), _bits(qr.contiguous()))
+    if with_q:
+        assert torch.equal(_bits(qo.cpu()), _bits(qr.contiguous()))
+    else:
+        assert qo is None
     assert torch.equal(_bits(g.kv_cache.cpu()), _bits(want))
 
 
@@ -94,3 +99,28 @@ def test_rope_append_fused_projection_views():
 
 def test_rope_append_single_token():
     _parity(wl.decode_case(wl.QWEN2_7B, [77], seed=206))
+
+
+@pytest.mark.parametrize("cfg", ["qwen2-0.5b-decode", "llama3-8b-decode", "qwen2-7b-prefill"])
+def test_k_only_form_named_cases(cfg):
+    _parity(wl.config_case(cfg), base=500000.0 if cfg.startswith("llama") else 1e6,
+            with_q=False)
+
+
+def test_k_only_form_edges():
+    # prefixes and empty prompts; the column clamp; more than 63 prompts (the binary-search
+    # lookup); one token; strided k/v views; head_dim 64
+    _parity(wl.prefill_case(wl.QWEN2_7B, [5, 0, 33, 17, 1, 0], seed=207,
+                            ctx_lens=[0, 3, 14, 16, 100, 0]), with_q=False)
+    case = wl.prefill_case(wl.QWEN2_05B, [3, 5], seed=208, ctx_lens=[16, 40])
+    case.block_table = case.block_table[:, :1].contiguous()
+    _parity(case, with_q=False)
+    lens = [1 + (7 * i) % 23 for i in range(80)]
+    _parity(wl.prefill_case(wl.QWEN2_05B, lens, seed=209), with_q=False)
+    _parity(wl.decode_case(wl.QWEN2_7B, [77], seed=210), with_q=False)
+    case = wl.prefill_case(wl.LLAMA3_8B, [7, 40, 16], seed=211)
+    t, h, d = case.q.shape
+    hkv = case.k.shape[1]
+    fused = torch.randn((t, (h + 2 * hkv) * d)).to(torch.bfloat16)
+    _parity(case, base=500000.0, k=fused[:, h * d:(h + hkv) * d].view(t, hkv, d),
+            v=fused[:, (h + hkv) * d:].view(t, hkv, d), with_q=False)
