@@ -71,9 +71,34 @@ __device__ __forceinline__ void rope8(const u32x4& lo, const u32x4& hi, const u3
 // exp2 on the hardware transcendental unit (v_exp_f32).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// Butterfly exchange across lanes (lane ^ mask) inside a wave64.
+// Butterfly exchange across lanes (lane ^ mask) inside a wave64 (ds_bpermute).
 __device__ __forceinline__ float xor_shfl(float v, int mask) {
   return __shfl_xor(v, mask, 64);
+}
+
+// v[l] op v[l ^ 16] and v[l] op v[l ^ 32] on the VALU: v_permlane16_swap / v_permlane32_swap
+// of a register with itself returns, in every lane, the pair's value of the lower row (or
+// half) in one result and of the upper one in the other, so both lanes of a pair combine
+// the same two values in the same order (no LDS crossbar round trip).
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 __device__ __forceinline__ u32x4 ldg16(const void* p) {

@@ -259,36 +259,60 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
   // NW-th in the per-sequence split); first_bt, if not null, holds this lane's block id of
   // the first window (column lt0 + NW * lane, clamped to the row), loaded by the caller.
   constexpr int stride = NW;
+
+  // B operand of S^T = K Q^T: lane (j, c) supplies Q[head c][32 s + 8 j .. +8), rotated
+  // (ROPE, attention.py:88, :277-283): the lane's element d = 32 s + 8 j + e pairs with
+  // d + D/2, which is the same lane's chunk s + KS/2.
+  auto load_q = [&](const int seq, bf16x8 (&qb)[KS]) {
+    // Lanes past the group read the group's first head (no branch around the loads, so the
+    // compiler can count them) and zero it.
+    const u16* qrow = a.q + (int64_t)seq * a.q_tok_stride +
+                      (int64_t)(head_ok ? head : kvh * a.group) * D + 8 * j;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const u32x4 w = ld16(qrow + 32 * s);
+      qb[s] = __builtin_bit_cast(bf16x8, head_ok ? w : u32x4{0u, 0u, 0u, 0u});
+    }
+    if constexpr (ROPE) {
+      const u16* crow = a.rope_cos + (int64_t)seq * a.rope_stride + 8 * j;
+      const u16* srow = a.rope_sin + (int64_t)seq * a.rope_stride + 8 * j;
+      u32x4 rc[KS], rs[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        rc[s] = ld16(crow + 32 * s);
+        rs[s] = ld16(srow + 32 * s);
+      }
+#pragma unroll
+      for (int s = 0; s < KS / 2; ++s) {
+        u32x4 lo, hi;
+        rope8(__builtin_bit_cast(u32x4, qb[s]), __builtin_bit_cast(u32x4, qb[s + KS / 2]),
+              rc[s], rc[s + KS / 2], rs[s], rs[s + KS / 2], lo, hi);
+        qb[s] = __builtin_bit_cast(bf16x8, lo);
+        qb[s + KS / 2] = __builtin_bit_cast(bf16x8, hi);
+      }
+    }
+  };
+
+  // K (in row layout, staged through LDS) and V of the tile at block id blk.  An invalid
+  // id reads block 0 (always mapped) and marks the tile bad.
+  auto load_tile_blk = [&](int64_t blk, Tile& t) {
+    t.bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
+    if (t.bad) blk = 0;
+    const u16* kb = a.kplane + blk * blk_stride + head_off;
+    const u16* vb = a.vplane + blk * blk_stride + head_off;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) t.k[s] = ldg16(kb + k_off + RPI * D * s);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t.v[i] = load_vrow<D>(vb + v_off + i * D);
+  };
+
   auto segment = [&](const int seq, const int lt0, const int lt1, const int n_tiles,
                      const int segid, const int* first_bt) {
     const int64_t L = attended_len(a, seq);
     const int t1 = (int)(lt1 * 16 < L ? lt1 * 16 : L);   // one past the last token attended
 
-    // B operand of S^T = K Q^T: lane (j, c) supplies Q[head c][32 s + 8 j .. +8).
     bf16x8 qb[KS];
-    {
-      const u16* qrow = a.q + (int64_t)seq * a.q_tok_stride + (int64_t)head * D + 8 * j;
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        u32x4 w = head_ok ? ld16(qrow + 32 * s) : u32x4{0u, 0u, 0u, 0u};
-        qb[s] = __builtin_bit_cast(bf16x8, w);
-      }
-    }
-    if constexpr (ROPE) {
-      // RoPE of q (attention.py:88, :277-283): the lane's element d = 32 s + 8 j + e pairs
-      // with d + D/2, which is the same lane's chunk s + KS/2.
-      const u16* crow = a.rope_cos + (int64_t)seq * a.rope_stride + 8 * j;
-      const u16* srow = a.rope_sin + (int64_t)seq * a.rope_stride + 8 * j;
-#pragma unroll
-      for (int s = 0; s < KS / 2; ++s) {
-        u32x4 lo, hi;
-        rope8(__builtin_bit_cast(u32x4, qb[s]), __builtin_bit_cast(u32x4, qb[s + KS / 2]),
-              ld16(crow + 32 * s), ld16(crow + 32 * (s + KS / 2)), ld16(srow + 32 * s),
-              ld16(srow + 32 * (s + KS / 2)), lo, hi);
-        qb[s] = __builtin_bit_cast(bf16x8, lo);
-        qb[s + KS / 2] = __builtin_bit_cast(bf16x8, hi);
-      }
-    }
+    load_q(seq, qb);
     const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
 
     // Fused append (attention.py:141-154 before :156-159): the new token of the step sits
@@ -340,17 +364,13 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       const int ntiles = left < 64 ? left : 64;
       const int bt_lane = (first_bt != nullptr && w0 == lt0) ? *first_bt
                           : lane < ntiles ? bt_row[w0 + stride * lane] : 0;
+      // The window's ids are waited for here, once: a use inside the tile ring below would
+      // otherwise wait for every load in flight (the compiler cannot tell which load the
+      // register came from on the loop's first trip), emptying the ring at each tile.
+      asm volatile("" ::"v"(bt_lane));
 
       auto load_tile = [&](int it, Tile& t) {
-        int64_t blk = __builtin_amdgcn_readlane(bt_lane, it);
-        t.bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
-        if (t.bad) blk = 0;
-        const u16* kb = a.kplane + blk * blk_stride + head_off;
-        const u16* vb = a.vplane + blk * blk_stride + head_off;
-#pragma unroll
-        for (int s = 0; s < KS; ++s) t.k[s] = ldg16(kb + k_off + RPI * D * s);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) t.v[i] = load_vrow<D>(vb + v_off + i * D);
+        load_tile_blk(__builtin_amdgcn_readlane(bt_lane, it), t);
       };
 
       auto compute_tile = [&](int it, Tile& t) {
@@ -400,8 +420,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
           sc[i] = ok ? st[i] * a.scale_log2 : kNegInf;
           mt = fmaxf(mt, sc[i]);
         }
-        mt = fmaxf(mt, xor_shfl(mt, 16));
-        mt = fmaxf(mt, xor_shfl(mt, 32));
+        mt = max_xor32(max_xor16(mt));
         const float m_new = fmaxf(m, mt);
         const float m_use = m_new == kNegInf ? 0.f : m_new;
         const float alpha = fast_exp2(m - m_use);
@@ -453,8 +472,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       }
     }
 
-    lsum += xor_shfl(lsum, 16);
-    lsum += xor_shfl(lsum, 32);
+    lsum = add_xor32(add_xor16(lsum));
     if (!head_ok) return;
 
     // acc[b][i] holds O[head c][d = DPL * (4 j + i) + b].
@@ -518,7 +536,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         const int64_t t0 = first + kStreamPad;   // the sequence's first tile
         const int64_t s0 = start > t0 ? start : t0;
         const int64_t s1 = end < t0 + nt ? end : t0 + nt;
-        if (s1 > s0) segment(seq, (int)(s0 - t0), (int)(s1 - t0), nt, sw + seq, nullptr);
+        if (s1 > s0)
+          segment(seq, (int)(s0 - t0), (int)(s1 - t0), nt, sw + seq, nullptr);
       }
       first += stream_slots(nt);
       ++seq;
@@ -533,39 +552,40 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         a.block_table[(int64_t)seq * a.bt_row_stride + (col < a.max_blocks ? col : a.max_blocks - 1)];
     const int nt = seq_tiles(a, seq);
     if (wv < nt) segment(seq, wv, nt, nt, 0, &first_bt);
-    // Combine: every wave's (m, l) and accumulators to LDS (the K tiles are dead once
-    // all waves are past their loop), then wave w finishes elements w*KPW .. + KPW of
-    // every lane over the NW waves in a fixed order.  A sequence with nothing to attend
-    // (no tiles) comes out as zeros (attention.py:307-308 on an empty context).
+    // Combine: every wave's m to LDS; each lane takes the maximum M over the waves for its
+    // head and scales its wave's accumulators and l by 2^(m - M) (one exponential per lane)
+    // into LDS (over the K tiles, dead once every wave is past the first barrier); then wave
+    // w sums elements w*KPW .. + KPW of every lane over the NW waves in a fixed order.  A
+    // sequence with nothing to attend (no tiles) comes out as zeros (attention.py:307-308 on
+    // an empty context).
+    static_assert(NW * 16 * D * 2 <= NW * 64 * E * 4, "m is stored past the K tiles");
     constexpr int KPW = E / NW;
     static_assert(KPW * NW == E, "waves must divide the accumulator elements");
-    float* const sacc = smem;                 // [wave][E][64]
-    float* const sml = smem + NW * 64 * E;    // [wave][2][16]
+    float* const sacc = smem;                 // [wave][E][64]: scaled accumulators
+    float* const sm = smem + NW * 64 * E;     // [wave][16]: m
+    float* const sl = sm + NW * 16;           // [wave][16]: scaled l
+    if (j == 0) sm[wv * 16 + c] = held_m;
     __syncthreads();
+    float mx = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm[w * 16 + c]);
+    const float wt = held_m == kNegInf ? 0.f : fast_exp2(held_m - mx);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int b = 0; b < DPL; ++b) sacc[(wv * E + DPL * i + b) * 64 + lane] = held[b][i];
+      for (int b = 0; b < DPL; ++b) sacc[(wv * E + DPL * i + b) * 64 + lane] = held[b][i] * wt;
     }
-    if (j == 0) {
-      sml[wv * 32 + c] = held_m;
-      sml[wv * 32 + 16 + c] = held_l;
-    }
+    if (j == 0) sl[wv * 16 + c] = held_l * wt;
     __syncthreads();
     if (!head_ok) return;
-    float mx = kNegInf;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sml[w * 32 + c]);
     float den = 0.f, o[KPW];
 #pragma unroll
     for (int k = 0; k < KPW; ++k) o[k] = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      const float mw = sml[w * 32 + c];
-      const float wt = mw == kNegInf ? 0.f : fast_exp2(mw - mx);
-      den += wt * sml[w * 32 + 16 + c];
+      den += sl[w * 16 + c];
 #pragma unroll
-      for (int k = 0; k < KPW; ++k) o[k] += wt * sacc[(w * E + wv * KPW + k) * 64 + lane];
+      for (int k = 0; k < KPW; ++k) o[k] += sacc[(w * E + wv * KPW + k) * 64 + lane];
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
     u16* const out_row =
