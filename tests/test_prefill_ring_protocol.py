@@ -12,6 +12,15 @@ comes after the clear, each wait count is exact, and each wave's output plane is
 wave reads after the tile's last barrier.  Changing the schedule in the kernel means changing
 it here too; a plausible slip (a wait one step short, a slot refilled one step early, the odd
 last step without its barrier) fails one of the checks (see test_model_catches_slips).
+
+The tile prologue is the kernel's: after the barrier that retires the previous tile's reads,
+steps 0 and 1 are staged, each wave stages its 32 Q rows into one plane of slots 2 .. 5 (wave
+w: slot 2 + w // 2, the K plane for even w, else the V plane), waits for all its loads, reads
+its Q plane back (with RoPE, rotates it in place first), and the next barrier publishes steps
+0 and 1 and retires the Q reads; only then are steps 2 .. NS - 3 staged.  The fast trips are
+steady trips whose load wait is the constant (NS - 5) steps (the ring in full flow: both steps
+they stage exist, and step t + 2, which they publish, needs no clearing).  A wave that skips
+the reads of steps past its last query row only removes reads, which no check depends on.
 """
 import random
 
@@ -20,16 +29,28 @@ import pytest
 PAIR, FIRST, SECOND, NONE = "pair", "first", "second", "none"
 
 
+WAVES = 8
+Q = -1    # the "step" of a Q staging write / read
+
+
+def q_plane(w):
+    """The prologue's Q staging plane of wave w: (slot, plane)."""
+    return 2 + w // 2, "K" if w % 2 == 0 else "V"
+
+
 class Ring:
-    def __init__(self, nsteps, ns, vzero, wait_slip=0, stage_slip=0):
+    def __init__(self, nsteps, ns, vzero, wait_slip=0, stage_slip=0, q_slot_slip=0,
+                 early_stage=False, fast_wait_slip=0):
         self.n, self.ns, self.vzero = nsteps, ns, vzero
         self.wait_slip, self.stage_slip = wait_slip, stage_slip
+        self.q_slot_slip, self.early_stage = q_slot_slip, early_stage
+        self.fast_wait_slip = fast_wait_slip
         self.interval = 0
         self.issued = []          # steps in load-issue order (one loader queue)
         self.published = {}       # step -> first interval in which its loads are visible
         self.cleared = {}         # step -> interval of its V clear
-        self.writes = []          # (interval, slot, step, what)
-        self.reads = []           # (interval, slot, step, plane)
+        self.writes = []          # (interval, slot, step, what); Q writes: what = ("q", w, plane)
+        self.reads = []           # (interval, slot, step, plane); Q reads: step = Q, plane (Q, w, plane)
 
     # -- kernel primitives -------------------------------------------------------------
     def stage(self, x):
@@ -84,11 +105,16 @@ class Ring:
             if need > t and self.vzero[need]:
                 self.clear(need)
 
-    def steady(self, t):
-        """The steady-state trip: steps t and t + 1 under one barrier."""
+    def steady(self, t, fast=False):
+        """The steady-state trip: steps t and t + 1 under one barrier.  fast: the kernel's
+        fast trip, which waits for the constant NS - 5 later steps without computing it."""
         n, ns = self.n, self.ns
         need = min(t + 2, n - 1)
-        later = ns - 5 if t + ns - 3 <= n - 1 else n - 1 - need
+        if fast:
+            assert t + ns - 1 < n and not self.vzero[t + 2], "fast trip outside its range"
+            later = ns - 5 + self.fast_wait_slip
+        else:
+            later = ns - 5 if t + ns - 3 <= n - 1 else n - 1 - need
         self.expect_later(need, later)
         self.wait(later)
         self.barrier()
@@ -100,20 +126,41 @@ class Ring:
         self.step_reads(t)
         self.step_reads(t + 1)
 
-    def run(self, steady_lim=0, odd_tail_barrier=True):
+    def prologue(self):
         n, ns = self.n, self.ns
         self.barrier()                            # retire the previous tile's reads
-        for t in range(min(ns - 2, n)):
-            self.stage(t)
-        self.wait(min(n - 1, ns - 3))
-        self.barrier()
+        self.stage(0)
+        if n > 1:
+            self.stage(1)
+        if self.early_stage:                      # slip: steps 2 .. NS-3 before the Q reads retire
+            for t in range(2, min(ns - 2, n)):
+                self.stage(t)
+        for w in range(WAVES):
+            slot, plane = q_plane(w)
+            slot = (slot + self.q_slot_slip) % ns
+            self.writes.append((self.interval, slot, Q, ("q", w, plane)))
+        self.wait(0)                              # each wave: all its loads landed
+        for w in range(WAVES):
+            slot, plane = q_plane(w)
+            slot = (slot + self.q_slot_slip) % ns
+            self.writes.append((self.interval, slot, Q, ("rope", w, plane)))   # in place
+            self.reads.append((self.interval, slot, Q, ("Q", w, plane)))
+        self.barrier()                            # publishes steps 0, 1; retires the Q reads
+        if not self.early_stage:
+            for t in range(2, min(ns - 2, n)):
+                self.stage(t)
         if self.vzero[0]:
             self.clear(0)
         self.read(0, "K")
+
+    def run(self, steady_lim=0, odd_tail_barrier=True, fast_trips=False):
+        n, ns = self.n, self.ns
+        self.prologue()
         t = 0
         while t < steady_lim:
             assert not self.vzero[t] and not self.vzero[t + 1]
-            self.steady(t)
+            fast = fast_trips and t + ns - 1 < n and not self.vzero[t + 2]
+            self.steady(t, fast=fast)
             t += 2
         while t + 2 <= n:
             if not self.vzero[t + 1]:
@@ -128,20 +175,45 @@ class Ring:
         return self
 
     # -- checks ------------------------------------------------------------------------
+    @staticmethod
+    def _planes(what):
+        """Planes a write touches: a step's load both, a clear V, a Q write its own."""
+        if what == "load":
+            return {"K", "V"}
+        if what == "clear":
+            return {"V"}
+        return {what[2]}
+
     def check(self):
         n = self.n
         assert sorted(self.issued) == list(range(n)), f"issued {self.issued}"
         for (iv, slot, x, plane) in self.reads:
+            if x == Q:
+                # a wave's own Q plane, read after its own wait in the interval it was written
+                mine = [w for w in self.writes if w[1] == slot and w[0] == iv and w[2] == Q
+                        and w[3][1] == plane[1] and w[3][2] == plane[2]]
+                assert mine, f"wave {plane[1]} reads a Q plane it did not stage"
+                continue
             if x >= n:
                 continue                          # QK past the last step: never used
-            earlier = [w for w in self.writes if w[1] == slot and w[3] == "load" and w[0] < iv]
+            earlier = [w for w in self.writes if w[1] == slot and w[0] < iv and
+                       plane in self._planes(w[3]) and w[3] != "clear"]
             assert earlier and earlier[-1][2] == x, f"{plane} of step {x} read from a stale slot"
             assert self.published.get(x, 1 << 30) <= iv, f"{plane} of step {x} read before publish"
             if plane == "V" and self.vzero[x]:
                 assert self.cleared.get(x, 1 << 30) < iv, f"V of step {x} read before its clear"
         for (iv, slot, x, what) in self.writes:
             for (riv, rslot, y, plane) in self.reads:
-                if riv == iv and rslot == slot and y < n and (what == "load" or plane == "V"):
+                if riv != iv or rslot != slot:
+                    continue
+                if y == Q:
+                    rp = plane[2]
+                    if rp not in self._planes(what):
+                        continue
+                    if x == Q and what[1] == plane[1]:
+                        continue                  # the wave's own staging / rotation
+                    raise AssertionError(f"{what} of step {x} races wave {plane[1]}'s Q read")
+                if y < n and (what == "load" or plane == "V") and plane in self._planes(what):
                     raise AssertionError(f"{what} of step {x} races a {plane} read of step {y}")
         return self
 
@@ -172,13 +244,15 @@ def cases(seed=1):
                 yield ns, n, vz, lim
 
 
-@pytest.mark.parametrize("ns", [5, 6, 7, 8])
-def test_ring_schedule_orders_every_access(ns):
+@pytest.mark.parametrize("ns", [6, 7, 8])
+@pytest.mark.parametrize("fast", [False, True])
+def test_ring_schedule_orders_every_access(ns, fast):
+    # NS >= 6: the Q staging needs slots 2 .. 5 (the kernel asserts NS >= 2 + 8 / 2)
     count = 0
     for r_ns, n, vz, lim in cases():
         if r_ns != ns:
             continue
-        ring = Ring(n, ns, vz).run(steady_lim=lim).check()
+        ring = Ring(n, ns, vz).run(steady_lim=lim, fast_trips=fast).check()
         if 2 * ns - 3 >= 8:                        # the kernel asserts this for its output planes
             busy = ring.reads_after_last_barrier()
             planes = [output_plane(w, n, ns) for w in range(8)]
@@ -191,13 +265,21 @@ def test_ring_schedule_orders_every_access(ns):
 def test_model_catches_slips():
     """Each plausible schedule mistake fails some check on some case."""
     def fails(**kw):
-        run_kw = {"odd_tail_barrier": kw.pop("odd_tail_barrier", True)}
+        run_kw = {"odd_tail_barrier": kw.pop("odd_tail_barrier", True),
+                  "fast_trips": kw.pop("fast_trips", False)}
         for ns, n, vz, lim in cases(seed=2):
+            if ns < 6:
+                continue
             try:
                 Ring(n, ns, vz, **kw).run(steady_lim=lim, **run_kw).check()
             except AssertionError:
                 return True
         return False
+    assert not fails(), "the kernel's schedule itself passes"
+    assert not fails(fast_trips=True)
     assert fails(wait_slip=1), "a wait that leaves one step too many out"
     assert fails(stage_slip=-1), "a slot refilled one step early"
     assert fails(odd_tail_barrier=False), "the odd last step without its barrier"
+    assert fails(q_slot_slip=-1), "Q staged over step 1's slot"
+    assert fails(early_stage=True), "steps 2 .. NS-3 staged before the Q reads retire"
+    assert fails(fast_wait_slip=1, fast_trips=True), "a fast trip waiting one step short"
