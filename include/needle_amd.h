@@ -67,6 +67,8 @@ enum ndl_status {
 /* Size of the per-device static scratch array of ndl_paged_decode_append_noalloc. */
 #define NDL_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
 
+/* Element format of the pools and activations: the model dtypes the reference runs its
+ * attention in (needle/args.py:80-84; float32 is not built).  Every entry point takes both. */
 enum ndl_dtype {
   NDL_DTYPE_BF16 = 0,
   NDL_DTYPE_F16 = 1
@@ -113,13 +115,14 @@ int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int bloc
  *
  * For every token t and every element d < head_dim, with half = head_dim / 2,
  *   rot(x)[d] = -x[d + half] (d < half), x[d - half] (d >= half)
- *   y[d]      = bf16( bf16(x[d] * cos[t][d]) + bf16(rot(x)[d] * sin[t][d]) )
- * which is the reference's op-by-op bf16 rounding (bit-exact).  q rotated is
+ *   y[d]      = r( r(x[d] * cos[t][d]) + r(rot(x)[d] * sin[t][d]) )
+ * with r the rounding to the element format (bf16 or fp16, nearest even), which is the
+ * reference's op-by-op rounding in the model dtype (bit-exact).  q rotated is
  * written to q_out [num_tokens][num_heads][head_dim] (contiguous); k rotated and
  * v unchanged go to the cache slot that ndl_kv_append would pick for token t
  * (same slot rule, same handling of out-of-range block ids).  cos/sin:
  * [num_tokens][head_dim] with token stride cs_tok_stride.  head_dim must be a
- * multiple of 16; bf16 only.  q and q_out may both be NULL: then only k is rotated and
+ * multiple of 16.  q and q_out may both be NULL: then only k is rotated and
  * k, v appended (for ndl_rope_varlen_prefill, which rotates q itself).
  */
 int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stride,
@@ -158,7 +161,7 @@ size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_
  *   out[i][h][:] = softmax(scale * q[i][h] . K_i^T) V_i            (:307-308)
  * q: [num_seqs][num_heads][head_dim], token stride q_tok_stride.
  * out: [num_seqs][num_heads][head_dim] contiguous.  fp32 accumulation.
- * L_i <= 0 gives zeros.  Supported: bf16, block_size 16, head_dim 64 or 128,
+ * L_i <= 0 gives zeros.  Supported: bf16 and fp16, block_size 16, head_dim 64 or 128,
  * num_heads / num_kv_heads in 1..16.  The workspace (ndl_paged_decode_workspace_bytes)
  * is always required; calls that share one must not overlap.
  */
@@ -208,7 +211,7 @@ int ndl_paged_decode_append(void* out, const void* q, int64_t q_tok_stride,
  *
  * q, k: as produced by the projections, NOT rotated.  cos/sin: [num_seqs][head_dim] rows
  * of the new tokens (the model's get_cos_sin(positions)), token stride cs_tok_stride.  The
- * rotation is ndl_rope_kv_append's, bit for bit (the reference's bf16 rounding op for op),
+ * rotation is ndl_rope_kv_append's, bit for bit (the reference's rounding op for op),
  * so the cache bytes and out equal those of ndl_rope_kv_append (decode form) followed by
  * ndl_paged_decode with the rotated q.  Everything else as ndl_paged_decode_append.
  */

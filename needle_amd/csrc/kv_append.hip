@@ -46,8 +46,9 @@ constexpr int kAppendSmallSeqs = 63;
 // ROPE: k is rotated on the way (the rotary embedding of ndl_rope_kv_append, rope8, from
 // the token's cos/sin rows).  A lane then moves a chunk pair (c, c + head_dim/16) of one
 // row, the rotation's operands: items are the k rows' pairs, then the v rows' pairs (copied
-// unrotated), the same count as the chunks of one plane without ROPE.
-template <int TPW, bool SMALL, bool ROPE>
+// unrotated), the same count as the chunks of one plane without ROPE.  F16: the rotation's
+// element format is fp16 (else bf16); the plain copy is format-free.
+template <int TPW, bool SMALL, bool ROPE, bool F16 = false>
 __global__ __launch_bounds__(256) void kv_append_kernel(
     u16* __restrict__ cache, int64_t plane_elems, int64_t num_blocks, int num_kv_heads,
     int block_size, int head_dim,
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 #pragma unroll
     for (int u = 0; u < TPW; ++u) {
       u32x4 ol = xl[u], oh = xh[u];
-      if (!is_v) rope8(xl[u], xh[u], cl[u], ch[u], sl[u], sh[u], ol, oh);
+      if (!is_v) rope8<F16>(xl[u], xh[u], cl[u], ch[u], sl[u], sh[u], ol, oh);
       if (live && dst_row[u] >= 0) {
         st16(plane + dst_row[u] + out_off, ol);
         st16(plane + dst_row[u] + out_off + half * 8, oh);
@@ -184,14 +185,15 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 }
 
 // Shared by ndl_kv_append and the k-only form of ndl_rope_kv_append (rope_cos != nullptr:
-// k rotated; head_dim a multiple of 16).  Arguments are checked by the callers.
+// k rotated in the format of rope_f16; head_dim a multiple of 16).  Arguments are checked by
+// the callers.
 int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int block_size,
                      int head_dim, const void* k, int64_t k_tok_stride, const void* v,
                      int64_t v_tok_stride, const int32_t* block_table, int64_t bt_row_stride,
                      int max_blocks_per_seq, const int32_t* cu_seqlens,
                      const int32_t* context_lens, int num_seqs, int64_t num_tokens,
                      const void* rope_cos, const void* rope_sin, int64_t rope_stride,
-                     ndl_stream_t stream) {
+                     bool rope_f16, ndl_stream_t stream) {
   const int64_t plane_elems = num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
   const bool small = cu_seqlens != nullptr && num_seqs <= kAppendSmallSeqs;
   const bool rope = rope_cos != nullptr;
@@ -206,12 +208,14 @@ int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int b
   const int64_t waves = (num_tokens + tpw - 1) / tpw;
   const int64_t blocks = (waves + 3) / 4;
   if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
-#define NDL_APPEND_FNS(S, R)                                                          \
-  {(const void*)kv_append_kernel<1, S, R>, (const void*)kv_append_kernel<2, S, R>,    \
-   (const void*)kv_append_kernel<3, S, R>, (const void*)kv_append_kernel<4, S, R>}
-  const void* fns[2][2][kAppendMaxTokensPerWave] = {
-      {NDL_APPEND_FNS(false, false), NDL_APPEND_FNS(true, false)},
-      {NDL_APPEND_FNS(false, true), NDL_APPEND_FNS(true, true)}};
+#define NDL_APPEND_FNS(S, R, F)                                                           \
+  {(const void*)kv_append_kernel<1, S, R, F>, (const void*)kv_append_kernel<2, S, R, F>,  \
+   (const void*)kv_append_kernel<3, S, R, F>, (const void*)kv_append_kernel<4, S, R, F>}
+  // [copy, rotate bf16, rotate fp16][small][tokens per wave - 1]
+  const void* fns[3][2][kAppendMaxTokensPerWave] = {
+      {NDL_APPEND_FNS(false, false, false), NDL_APPEND_FNS(true, false, false)},
+      {NDL_APPEND_FNS(false, true, false), NDL_APPEND_FNS(true, true, false)},
+      {NDL_APPEND_FNS(false, true, true), NDL_APPEND_FNS(true, true, true)}};
 #undef NDL_APPEND_FNS
   u16* cache = (u16*)kv_cache;
   const u16* kp = (const u16*)k;
@@ -222,7 +226,8 @@ int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int b
                   &head_dim, &kp, &k_tok_stride, &vp, &v_tok_stride, &block_table,
                   &bt_row_stride, &max_blocks_per_seq, &cu_seqlens, &context_lens, &num_seqs,
                   &num_tokens, &cp, &sp, &rope_stride};
-  if (hipLaunchKernel(fns[rope ? 1 : 0][small ? 1 : 0][tpw - 1], dim3((unsigned)blocks),
+  if (hipLaunchKernel(fns[rope ? (rope_f16 ? 2 : 1) : 0][small ? 1 : 0][tpw - 1],
+                      dim3((unsigned)blocks),
                       dim3(256), args, 0, (hipStream_t)stream) != hipSuccess) {
     (void)hipGetLastError();  // clear the error so that the next call's check sees its own
     return NDL_ERR_LAUNCH;
@@ -260,5 +265,5 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
   return launch_kv_append(kv_cache, num_blocks, num_kv_heads, block_size, head_dim, k,
                           k_tok_stride, v, v_tok_stride, block_table, bt_row_stride,
                           max_blocks_per_seq, cu_seqlens, context_lens, num_seqs, num_tokens,
-                          nullptr, nullptr, 0, stream);
+                          nullptr, nullptr, 0, false, stream);
 }

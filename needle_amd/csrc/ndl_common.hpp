@@ -43,29 +43,99 @@ __device__ __forceinline__ uint32_t pack_halves(uint32_t lo, uint32_t hi, bool h
   return __builtin_amdgcn_perm(hi, lo, high_half ? 0x07060302u : 0x05040100u);
 }
 
-// Rotary embedding with the reference's rounding (attention.py:277-288, op for op in bf16):
-//   out[d] = bf16( bf16(x[d] * cos[d]) + bf16(rot(x)[d] * sin[d]) ),
+typedef __attribute__((ext_vector_type(16))) float f32x16;
+typedef __attribute__((ext_vector_type(8))) _Float16 f16x8;
+typedef __attribute__((ext_vector_type(4))) _Float16 f16x4;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
+
+// The 16-bit element format of the pools and activations: bfloat16 (Elt<false>) or
+// float16 (Elt<true>), the model dtypes the reference runs its attention in
+// (needle/args.py:80-84).  Elements are moved as raw bits; these are the only places the
+// format matters: conversions (fp32 <-> 16 bits, round to nearest even) and the MFMA
+// instructions.
+template <bool kF16> struct Elt;
+template <> struct Elt<false> {
+  using x8 = bf16x8;                                   // 8-element MFMA operand
+  static __device__ __forceinline__ float lo(uint32_t w) { return bf16_lo(w); }
+  static __device__ __forceinline__ float hi(uint32_t w) { return bf16_hi(w); }
+  static __device__ __forceinline__ uint32_t pack(float a, float b) { return pack_bf16x2(a, b); }
+  static __device__ __forceinline__ u16 one(float a) { return (u16)f32_to_bf16_bits(a); }
+  static __device__ __forceinline__ f32x16 mfma32x32x16(x8 a, x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16x16x32(x8 a, x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  // 4-element operands given as two words each
+  static __device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a),
+                                                     __builtin_bit_cast(i16x4, b), c, 0, 0, 0);
+  }
+};
+template <> struct Elt<true> {
+  using x8 = f16x8;
+  static __device__ __forceinline__ float lo(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (u16)(w & 0xffffu));
+  }
+  static __device__ __forceinline__ float hi(uint32_t w) {
+    return (float)__builtin_bit_cast(_Float16, (u16)(w >> 16));
+  }
+  static __device__ __forceinline__ uint32_t pack(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2{a, b}, f16x2));
+  }
+  static __device__ __forceinline__ u16 one(float a) {
+    return __builtin_bit_cast(u16, (_Float16)a);
+  }
+  static __device__ __forceinline__ f32x16 mfma32x32x16(x8 a, x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16x16x32(x8 a, x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mfma16x16x16(u32x2 a, u32x2 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a),
+                                                 __builtin_bit_cast(f16x4, b), c, 0, 0, 0);
+  }
+};
+
+// Rotary embedding with the reference's rounding (attention.py:277-288, op for op in the
+// model dtype):
+//   out[d] = r( r(x[d] * cos[d]) + r(rot(x)[d] * sin[d]) ),
 //   rot(x)[d] = -x[d + D/2] (d < D/2), x[d - D/2] (d >= D/2);
-// every product and the sum are formed in fp32 from bf16 operands and rounded to nearest
-// even, as torch does for bf16 tensors.
-// 8 bf16 of x[d..d+8) and x[d+D/2..d+D/2+8) -> rotated halves.  The two elements of a
-// word are rounded together (one v_cvt_pk_bf16_f32 per pair of products, each half rounded
+// every product and the sum are formed in fp32 from 16-bit operands and rounded (r) to the
+// element format, nearest even, as torch does for bf16 and fp16 tensors.
+// 8 elements of x[d..d+8) and x[d+D/2..d+D/2+8) -> rotated halves.  The two elements of a
+// word are rounded together (one packing conversion per pair of products, each half rounded
 // to nearest even on its own, exactly as two single roundings).
+// Contraction stays off: the fp32 product of two fp16 values is exact, so the compiler may
+// narrow product-then-round to an fp16 multiply, and with contraction on it would then fuse
+// that multiply into the sum (v_pk_fma_f16), skipping the product's rounding.
+template <bool kF16 = false>
 __device__ __forceinline__ void rope8(const u32x4& lo, const u32x4& hi, const u32x4& clo,
                                       const u32x4& chi, const u32x4& slo, const u32x4& shi,
                                       u32x4& out_lo, u32x4& out_hi) {
+#pragma clang fp contract(off)
+  using T = Elt<kF16>;
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
-    const float xl0 = bf16_lo(lo[w]), xl1 = bf16_hi(lo[w]);
-    const float xh0 = bf16_lo(hi[w]), xh1 = bf16_hi(hi[w]);
+    const float xl0 = T::lo(lo[w]), xl1 = T::hi(lo[w]);
+    const float xh0 = T::lo(hi[w]), xh1 = T::hi(hi[w]);
+    // -x_hi by its sign bits (exact, as the 16-bit negation of rotate_half)
+    const uint32_t nh = hi[w] ^ 0x80008000u;
     // first half: x*cos + (-x_hi)*sin ; second half: x_hi*cos + x*sin
-    const uint32_t p_xc = pack_bf16x2(xl0 * bf16_lo(clo[w]), xl1 * bf16_hi(clo[w]));
-    const uint32_t p_rs = pack_bf16x2(-xh0 * bf16_lo(slo[w]), -xh1 * bf16_hi(slo[w]));
-    const uint32_t p_hc = pack_bf16x2(xh0 * bf16_lo(chi[w]), xh1 * bf16_hi(chi[w]));
-    const uint32_t p_ls = pack_bf16x2(xl0 * bf16_lo(shi[w]), xl1 * bf16_hi(shi[w]));
-    out_lo[w] = pack_bf16x2(bf16_lo(p_xc) + bf16_lo(p_rs), bf16_hi(p_xc) + bf16_hi(p_rs));
-    out_hi[w] = pack_bf16x2(bf16_lo(p_hc) + bf16_lo(p_ls), bf16_hi(p_hc) + bf16_hi(p_ls));
+    const uint32_t p_xc = T::pack(xl0 * T::lo(clo[w]), xl1 * T::hi(clo[w]));
+    const uint32_t p_rs = T::pack(T::lo(nh) * T::lo(slo[w]), T::hi(nh) * T::hi(slo[w]));
+    const uint32_t p_hc = T::pack(xh0 * T::lo(chi[w]), xh1 * T::hi(chi[w]));
+    const uint32_t p_ls = T::pack(xl0 * T::lo(shi[w]), xl1 * T::hi(shi[w]));
+    out_lo[w] = T::pack(T::lo(p_xc) + T::lo(p_rs), T::hi(p_xc) + T::hi(p_rs));
+    out_hi[w] = T::pack(T::lo(p_hc) + T::lo(p_ls), T::hi(p_hc) + T::hi(p_ls));
   }
+}
+
+// The element format of an ABI dtype code (false: bf16, true: fp16); false for others.
+inline bool dtype_is_f16(int dtype) { return dtype == NDL_DTYPE_F16; }
+inline bool dtype_supported(int dtype) {
+  return dtype == NDL_DTYPE_BF16 || dtype == NDL_DTYPE_F16;
 }
 
 // exp2 on the hardware transcendental unit (v_exp_f32).
@@ -144,13 +214,14 @@ inline int64_t resident_workgroups(const void* fn, int block) {
   return wgs;
 }
 
-// The append launcher of kv_append.hip (rope_cos != nullptr: k rotated by rope8).
+// The append launcher of kv_append.hip (rope_cos != nullptr: k rotated by rope8 in the
+// format rope_f16 names).
 int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int block_size,
                      int head_dim, const void* k, int64_t k_tok_stride, const void* v,
                      int64_t v_tok_stride, const int32_t* block_table, int64_t bt_row_stride,
                      int max_blocks_per_seq, const int32_t* cu_seqlens,
                      const int32_t* context_lens, int num_seqs, int64_t num_tokens,
                      const void* rope_cos, const void* rope_sin, int64_t rope_stride,
-                     ndl_stream_t stream);
+                     bool rope_f16, ndl_stream_t stream);
 
 }  // namespace ndl

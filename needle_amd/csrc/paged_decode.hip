@@ -179,10 +179,13 @@ __device__ __forceinline__ int64_t stream_chunk(const DecodeArgs& a, int lane) {
 // sequence and the waves combine through LDS.
 // Two waves per SIMD for the default two-deep stream kernel (its 256-register budget), so
 // that the fused append's few extra registers do not halve its occupancy.
-template <int D, int NBUF, int NW, bool APP, bool ROPE = false>
+// F16: the elements are fp16 (else bf16).
+template <int D, int NBUF, int NW, bool APP, bool ROPE = false, bool F16 = false>
 __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     NW == 1 && NBUF == 2 ? 2 : 1))) void paged_decode_kernel(DecodeArgs a) {
   static_assert(APP || !ROPE, "the rotary form is a form of the fused append");
+  using T = Elt<F16>;
+  using X8 = typename T::x8;
   constexpr int KS = D / 32;   // k-steps of the QK^T MFMA
   constexpr int DPL = D / 16;  // head_dim elements per lane per V row
   constexpr int E = 4 * DPL;   // accumulator elements per lane (head_dim E*j .. + E of head c)
@@ -263,7 +266,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
   // B operand of S^T = K Q^T: lane (j, c) supplies Q[head c][32 s + 8 j .. +8), rotated
   // (ROPE, attention.py:88, :277-283): the lane's element d = 32 s + 8 j + e pairs with
   // d + D/2, which is the same lane's chunk s + KS/2.
-  auto load_q = [&](const int seq, bf16x8 (&qb)[KS]) {
+  auto load_q = [&](const int seq, X8 (&qb)[KS]) {
     // Lanes past the group read the group's first head (no branch around the loads, so the
     // compiler can count them) and zero it.
     const u16* qrow = a.q + (int64_t)seq * a.q_tok_stride +
@@ -271,7 +274,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       const u32x4 w = ld16(qrow + 32 * s);
-      qb[s] = __builtin_bit_cast(bf16x8, head_ok ? w : u32x4{0u, 0u, 0u, 0u});
+      qb[s] = __builtin_bit_cast(X8, head_ok ? w : u32x4{0u, 0u, 0u, 0u});
     }
     if constexpr (ROPE) {
       const u16* crow = a.rope_cos + (int64_t)seq * a.rope_stride + 8 * j;
@@ -285,10 +288,10 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
 #pragma unroll
       for (int s = 0; s < KS / 2; ++s) {
         u32x4 lo, hi;
-        rope8(__builtin_bit_cast(u32x4, qb[s]), __builtin_bit_cast(u32x4, qb[s + KS / 2]),
+        rope8<F16>(__builtin_bit_cast(u32x4, qb[s]), __builtin_bit_cast(u32x4, qb[s + KS / 2]),
               rc[s], rc[s + KS / 2], rs[s], rs[s + KS / 2], lo, hi);
-        qb[s] = __builtin_bit_cast(bf16x8, lo);
-        qb[s + KS / 2] = __builtin_bit_cast(bf16x8, hi);
+        qb[s] = __builtin_bit_cast(X8, lo);
+        qb[s + KS / 2] = __builtin_bit_cast(X8, hi);
       }
     }
   };
@@ -311,7 +314,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     const int64_t L = attended_len(a, seq);
     const int t1 = (int)(lt1 * 16 < L ? lt1 * 16 : L);   // one past the last token attended
 
-    bf16x8 qb[KS];
+    X8 qb[KS];
     load_q(seq, qb);
     const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
 
@@ -342,7 +345,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         const u16* crow = a.rope_cos + (int64_t)seq * a.rope_stride + 8 * lo_c;
         const u16* srow = a.rope_sin + (int64_t)seq * a.rope_stride + 8 * lo_c;
         u32x4 lo, hi;
-        rope8(first_half ? k_app : partner, first_half ? partner : k_app, ld16(crow),
+        rope8<F16>(first_half ? k_app : partner, first_half ? partner : k_app, ld16(crow),
               ld16(crow + 8 * HC), ld16(srow), ld16(srow + 8 * HC), lo, hi);
         k_app = first_half ? lo : hi;
       }
@@ -406,8 +409,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         for (int s = 0; s < KS; ++s) {
           const u32x4 ka =
               *reinterpret_cast<const u32x4*>(ktile + c * D + 8 * ((j + 4 * s) ^ swz(c)));
-          st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, ka), qb[s], st,
-                                                       0, 0, 0);
+          st = T::mfma16x16x32(__builtin_bit_cast(X8, ka), qb[s], st);
         }
         // st[i] is the score of token tix*16 + 4j + i for head c.
         const int pos0 = tix * 16 + 4 * j;
@@ -446,14 +448,12 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
           }
         }
 
-        const i16x4 pb = __builtin_bit_cast(
-            i16x4, u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])});
+        const u32x2 pb = {T::pack(p[0], p[1]), T::pack(p[2], p[3])};
 #pragma unroll
         for (int b = 0; b < DPL; ++b) {
           const uint32_t w01 = pack_halves(t.v[0][b >> 1], t.v[1][b >> 1], b & 1);
           const uint32_t w23 = pack_halves(t.v[2][b >> 1], t.v[3][b >> 1], b & 1);
-          acc[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(
-              __builtin_bit_cast(i16x4, u32x2{w01, w23}), pb, acc[b], 0, 0, 0);
+          acc[b] = T::mfma16x16x16(u32x2{w01, w23}, pb, acc[b]);
         }
       };
 
@@ -489,7 +489,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         uint32_t w[DPL / 2];
 #pragma unroll
         for (int b = 0; b < DPL; b += 2)
-          w[b / 2] = pack_bf16x2(acc[b][i] * inv, acc[b + 1][i] * inv);
+          w[b / 2] = T::pack(acc[b][i] * inv, acc[b + 1][i] * inv);
         if constexpr (DPL == 8)
           st16(out_row + DPL * i, u32x4{w[0], w[1], w[2], w[3]});
         else
@@ -591,11 +591,11 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     u16* const out_row =
         a.out + ((int64_t)seq * a.num_heads + head) * D + E * j + wv * KPW;
     if constexpr (KPW == 1) {
-      out_row[0] = (u16)f32_to_bf16_bits(o[0] * inv);
+      out_row[0] = T::one(o[0] * inv);
     } else {
       uint32_t w2[KPW / 2];
 #pragma unroll
-      for (int k = 0; k < KPW; k += 2) w2[k / 2] = pack_bf16x2(o[k] * inv, o[k + 1] * inv);
+      for (int k = 0; k < KPW; k += 2) w2[k / 2] = T::pack(o[k] * inv, o[k + 1] * inv);
       if constexpr (KPW == 4)
         *reinterpret_cast<u32x2*>(out_row) = u32x2{w2[0], w2[1]};
       else
@@ -616,7 +616,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
 constexpr int kMergeMaxParts = 2048;
 constexpr int kMergePrefetch = 8;
 
-template <int D>
+template <int D, bool F16>
 __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   constexpr int PER_LANE = D / 64;
   __shared__ float wsh[kMergeMaxParts];
@@ -648,7 +648,7 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
           const u16* crow = a.rope_cos + (int64_t)seq * a.rope_stride + 8 * lo_c;
           const u16* srow = a.rope_sin + (int64_t)seq * a.rope_stride + 8 * lo_c;
           u32x4 lo, hi;
-          rope8(first_half ? val : partner, first_half ? partner : val, ld16(crow),
+          rope8<F16>(first_half ? val : partner, first_half ? partner : val, ld16(crow),
                 ld16(crow + 8 * HC), ld16(srow), ld16(srow + 8 * HC), lo, hi);
           val = first_half ? lo : hi;
         }
@@ -750,9 +750,9 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
 
   const float inv = den > 0.f ? 1.f / den : 0.f;
   if constexpr (PER_LANE == 2)
-    *reinterpret_cast<uint32_t*>(dst) = pack_bf16x2(acc[0] * inv, acc[1] * inv);
+    *reinterpret_cast<uint32_t*>(dst) = Elt<F16>::pack(acc[0] * inv, acc[1] * inv);
   else
-    dst[0] = (u16)f32_to_bf16_bits(acc[0] * inv);
+    dst[0] = Elt<F16>::one(acc[0] * inv);
 }
 
 // Blocks in flight per wave (2..4).  NDL_DECODE_DEPTH overrides the default for tuning.
@@ -774,30 +774,43 @@ inline int64_t decode_resident_waves(const void* fn, int block = 64) {
 
 // APP: with the fused append (a separate instantiation, so that the attention-only kernel
 // carries none of its registers).
-template <int D, bool APP = false, bool ROPE = false> const void* decode_kernel_fn(int depth) {
-  return depth == 2 ? (const void*)paged_decode_kernel<D, 2, 1, APP, ROPE>
-                    : depth == 4 ? (const void*)paged_decode_kernel<D, 4, 1, APP, ROPE>
-                                 : (const void*)paged_decode_kernel<D, 3, 1, APP, ROPE>;
+// (The fp16 stream kernel is built at the default depth only.)
+template <int D, bool APP = false, bool ROPE = false, bool F16 = false>
+const void* decode_kernel_fn(int depth) {
+  if constexpr (F16) {
+    (void)depth;
+    return (const void*)paged_decode_kernel<D, 2, 1, APP, ROPE, true>;
+  } else {
+    return depth == 2 ? (const void*)paged_decode_kernel<D, 2, 1, APP, ROPE>
+                      : depth == 4 ? (const void*)paged_decode_kernel<D, 4, 1, APP, ROPE>
+                                   : (const void*)paged_decode_kernel<D, 3, 1, APP, ROPE>;
+  }
 }
-template <int D, bool APP = false, bool ROPE = false> const void* seq_split_kernel_fn() {
-  return (const void*)paged_decode_kernel<D, 2, seq_split_waves<D>(), APP, ROPE>;
+template <int D, bool APP = false, bool ROPE = false, bool F16 = false>
+const void* seq_split_kernel_fn() {
+  return (const void*)paged_decode_kernel<D, 2, seq_split_waves<D>(), APP, ROPE, F16>;
 }
 
-// The attention kernel for one call: head_dim, fused append, rotary form, split.
-inline const void* pick_decode_kernel(int head_dim, bool app, bool rope, bool seq_split,
-                                      int depth) {
-  if (seq_split) {
-    if (head_dim == 128)
-      return rope ? seq_split_kernel_fn<128, true, true>()
-                  : app ? seq_split_kernel_fn<128, true>() : seq_split_kernel_fn<128>();
-    return rope ? seq_split_kernel_fn<64, true, true>()
-                : app ? seq_split_kernel_fn<64, true>() : seq_split_kernel_fn<64>();
-  }
+template <int D, bool F16>
+inline const void* pick_decode_kernel_dt(bool app, bool rope, bool seq_split, int depth) {
+  if (seq_split)
+    return rope ? seq_split_kernel_fn<D, true, true, F16>()
+                : app ? seq_split_kernel_fn<D, true, false, F16>()
+                      : seq_split_kernel_fn<D, false, false, F16>();
+  return rope ? decode_kernel_fn<D, true, true, F16>(depth)
+              : app ? decode_kernel_fn<D, true, false, F16>(depth)
+                    : decode_kernel_fn<D, false, false, F16>(depth);
+}
+
+// The attention kernel for one call: head_dim, element format, fused append, rotary form,
+// split.
+inline const void* pick_decode_kernel(int head_dim, bool f16, bool app, bool rope,
+                                      bool seq_split, int depth) {
   if (head_dim == 128)
-    return rope ? decode_kernel_fn<128, true, true>(depth)
-                : app ? decode_kernel_fn<128, true>(depth) : decode_kernel_fn<128>(depth);
-  return rope ? decode_kernel_fn<64, true, true>(depth)
-              : app ? decode_kernel_fn<64, true>(depth) : decode_kernel_fn<64>(depth);
+    return f16 ? pick_decode_kernel_dt<128, true>(app, rope, seq_split, depth)
+               : pick_decode_kernel_dt<128, false>(app, rope, seq_split, depth);
+  return f16 ? pick_decode_kernel_dt<64, true>(app, rope, seq_split, depth)
+             : pick_decode_kernel_dt<64, false>(app, rope, seq_split, depth);
 }
 
 struct DecodeLayout {
@@ -937,11 +950,12 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
                          const void* v_new, int64_t v_new_stride, ndl_stream_t stream,
                          bool static_scratch = false, const void* rope_cos = nullptr,
                          const void* rope_sin = nullptr, int64_t rope_stride = 0) {
-  if (dtype != NDL_DTYPE_BF16) return NDL_ERR_UNSUPPORTED;
+  if (!dtype_supported(dtype)) return NDL_ERR_UNSUPPORTED;
   if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
     return NDL_ERR_INVALID_ARG;
   const int group = num_heads / num_kv_heads;
+  const bool f16 = dtype_is_f16(dtype);
   if (group > 16) return NDL_ERR_UNSUPPORTED;
   if (num_seqs < 0 || num_blocks <= 0 || max_blocks_per_seq <= 0 ||
       bt_row_stride < max_blocks_per_seq || q_tok_stride < (int64_t)num_heads * head_dim)
@@ -1008,14 +1022,14 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   const bool rope = rope_cos != nullptr;
   void* args[] = {&a};
   if (lay.seq_split) {  // one workgroup per (kv head, sequence), kv head fastest
-    const void* fn = pick_decode_kernel(head_dim, app, rope, true, 2);
+    const void* fn = pick_decode_kernel(head_dim, f16, app, rope, true, 2);
     if (hipLaunchKernel(fn, grid, dim3(64 * lay.seq_split), args, 0, s) != hipSuccess) {
       (void)hipGetLastError();
       return NDL_ERR_LAUNCH;
     }
     return check_launch();
   }
-  const void* fn = pick_decode_kernel(head_dim, app, rope, false, decode_pipeline_depth());
+  const void* fn = pick_decode_kernel(head_dim, f16, app, rope, false, decode_pipeline_depth());
   if (hipLaunchKernel(fn, grid, dim3(64), args, 0, s) != hipSuccess) {
     (void)hipGetLastError();
     return NDL_ERR_LAUNCH;
@@ -1024,9 +1038,11 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   if (rc != NDL_OK) return rc;
   const dim3 mgrid((unsigned)num_heads, (unsigned)num_seqs);
   if (head_dim == 128)
-    hipLaunchKernelGGL(paged_decode_merge_kernel<128>, mgrid, dim3(64), 0, s, a);
+    hipLaunchKernelGGL((f16 ? paged_decode_merge_kernel<128, true>
+                            : paged_decode_merge_kernel<128, false>), mgrid, dim3(64), 0, s, a);
   else
-    hipLaunchKernelGGL(paged_decode_merge_kernel<64>, mgrid, dim3(64), 0, s, a);
+    hipLaunchKernelGGL((f16 ? paged_decode_merge_kernel<64, true>
+                            : paged_decode_merge_kernel<64, false>), mgrid, dim3(64), 0, s, a);
   return check_launch();
 }
 

@@ -93,7 +93,6 @@ struct PrefTile {
   int tok0, tok1, ctx;
 };
 
-typedef __attribute__((ext_vector_type(16))) float f32x16;
 typedef __attribute__((ext_vector_type(4))) short i16x4v;
 
 // s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding:
@@ -178,9 +177,12 @@ __device__ __forceinline__ float half_sum(float v) {
 }
 
 // ROPE: q is the raw projection; each Q row is rotated as it is read into the operand
-// registers (with the reference's bf16 rounding, rope8), from cos/sin rows of its token.
-template <int D, int NS, bool ROPE>
+// registers (with the reference's rounding, rope8), from cos/sin rows of its token.
+// F16: the elements are fp16 (else bf16).
+template <int D, int NS, bool ROPE, bool F16>
 __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(PrefillArgs a) {
+  using T = Elt<F16>;
+  using X8 = typename T::x8;
   constexpr int KS = D / 16;          // k-steps of the QK MFMA (16 head_dim each)
   constexpr int DT = D / 32;          // 32-wide head_dim tiles of O^T
   constexpr int CPR = D / 8;          // 16-byte chunks per row
@@ -284,7 +286,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     // LDS at the ring start (below).  Loads issued after a step's (window refills) only
     // make a ring wait, which counts the direct loads issued after that step, wait longer,
     // never shorter: vector-memory loads complete in issue order.
-    bf16x8 qb[KS];
+    X8 qb[KS];
 
     // Every wave stages, per step, IPW of the PIECES / 2 pieces (1 KiB, one direct load
     // each) that block ld_blk of the step holds in plane ld_plane (K, V): pieces
@@ -389,8 +391,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       f32x16 st = {};
 #pragma unroll
       for (int s = 0; s < KS; ++s)
-        st = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, ka[s]), qb[s], st,
-                                                     0, 0, 0);
+        st = T::mfma32x32x16(__builtin_bit_cast(X8, ka[s]), qb[s], st);
       return st;
     };
     // P = exp2(s * scale log2e - m) rounded to bf16 (the B operand of the PV product);
@@ -404,7 +405,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       for (int r = 0; r < 16; r += 2) {
         p[r] = fast_exp2(fmaf(st[r], a.scale_log2, -m_use));
         p[r + 1] = fast_exp2(fmaf(st[r + 1], a.scale_log2, -m_use));
-        pw[r >> 1] = pack_bf16x2(p[r], p[r + 1]);
+        pw[r >> 1] = T::pack(p[r], p[r + 1]);
       }
 #pragma unroll
       for (int w = 8; w >= 1; w >>= 1)
@@ -414,7 +415,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     };
     // V^T operands of one step (all 16 transpose reads issued together, ahead of the
     // exponentials, so that no PV MFMA waits on LDS latency).
-    auto v_reads = [&](int stage, bf16x8* vop) {
+    auto v_reads = [&](int stage, X8* vop) {
       const u16* vt = lv[stage] + vlane;
 #pragma unroll
       for (int t = 0; t < 2; ++t)
@@ -426,18 +427,18 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
           const i16x4v v1 = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
               (__attribute__((address_space(3))) i16x4v*)(piece + 8 * 32));
           const u32x2 w0 = __builtin_bit_cast(u32x2, v0), w1 = __builtin_bit_cast(u32x2, v1);
-          vop[t * DT + dt] = __builtin_bit_cast(bf16x8, u32x4{w0[0], w0[1], w1[0], w1[1]});
+          vop[t * DT + dt] = __builtin_bit_cast(X8, u32x4{w0[0], w0[1], w1[0], w1[1]});
         }
     };
     // O^T += V^T P^T over the step's 32 keys.
-    auto pv = [&](const bf16x8* vop, const uint32_t* pw) {
+    auto pv = [&](const X8* vop, const uint32_t* pw) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const bf16x8 pb = __builtin_bit_cast(bf16x8, u32x4{pw[4 * t], pw[4 * t + 1],
-                                                           pw[4 * t + 2], pw[4 * t + 3]});
+        const X8 pb = __builtin_bit_cast(X8, u32x4{pw[4 * t], pw[4 * t + 1], pw[4 * t + 2],
+                                                   pw[4 * t + 3]});
 #pragma unroll
         for (int dt = 0; dt < DT; ++dt)
-          acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vop[t * DT + dt], pb, acc[dt], 0, 0, 0);
+          acc[dt] = T::mfma32x32x16(vop[t * DT + dt], pb, acc[dt]);
       }
     };
 
@@ -506,7 +507,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
 
     // Softmax and PV of one step whose scores are st (may_mask false: the caller knows
     // the step needs no mask).
-    auto finish = [&](int step, int stage, f32x16 st, const bf16x8* vop, bool may_mask) {
+    auto finish = [&](int step, int stage, f32x16 st, const X8* vop, bool may_mask) {
       const int kv0 = step * kPrefKeys;
       const bool masked = kv0 + kPrefKeys - 1 > qpos_min || kv0 + kPrefKeys > kv_end ||
                           ((badbits >> (2 * stage)) & 3u) != 0;
@@ -595,7 +596,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       // exactly when step + 1 will be.
       // (The V reads may follow the upkeep: it writes no slot of this step.)
       u32x4 ka[KS];
-      bf16x8 vop[2 * DT];
+      X8 vop[2 * DT];
       if ((step + 1) * kPrefKeys <= qpos_last) {
         k_reads(nstage, ka);
         st_next = qk(ka);
@@ -675,7 +676,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
         u32x4 lo = *reinterpret_cast<const u32x4*>(lo_at);
         u32x4 hi = *reinterpret_cast<const u32x4*>(hi_at);
         u32x4 rlo, rhi;
-        rope8(lo, hi, rcos[i][0], rcos[i][1], rsin[i][0], rsin[i][1], rlo, rhi);
+        rope8<F16>(lo, hi, rcos[i][0], rcos[i][1], rsin[i][0], rsin[i][1], rlo, rhi);
         *reinterpret_cast<u32x4*>(lo_at) = rlo;
         *reinterpret_cast<u32x4*>(hi_at) = rhi;
       }
@@ -686,7 +687,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
         const u32x4 w = *reinterpret_cast<const u32x4*>(&qplane[koff[s]]);
-        qb[s] = __builtin_bit_cast(bf16x8, ok ? w : u32x4{0u, 0u, 0u, 0u});
+        qb[s] = __builtin_bit_cast(X8, ok ? w : u32x4{0u, 0u, 0u, 0u});
       }
     }
     lds_barrier();
@@ -754,7 +755,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
             vm_wait<(NS - 5) * IPW>();
             lds_barrier();
             u32x4 ka[KS];
-            bf16x8 vop[2 * DT];
+            X8 vop[2 * DT];
             k_reads(stage1, ka);
             v_reads(stage, vop);
             st1 = qk(ka);
@@ -794,7 +795,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
         }
         lds_barrier();
         u32x4 ka[KS];
-        bf16x8 vop[2 * DT];
+        X8 vop[2 * DT];
         k_reads(stage1, ka);
         v_reads(stage, vop);
         st1 = qk(ka);
@@ -868,8 +869,8 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
 #pragma unroll
       for (int b = 0; b < 4; ++b)
         *reinterpret_cast<u32x2*>(piece + rr * D + 8 * ((4 * dt + b) ^ (rr % CPR)) + 4 * hh) =
-            u32x2{pack_bf16x2(acc[dt][4 * b] * inv, acc[dt][4 * b + 1] * inv),
-                  pack_bf16x2(acc[dt][4 * b + 2] * inv, acc[dt][4 * b + 3] * inv)};
+            u32x2{T::pack(acc[dt][4 * b] * inv, acc[dt][4 * b + 1] * inv),
+                  T::pack(acc[dt][4 * b + 2] * inv, acc[dt][4 * b + 3] * inv)};
     // Lane L reads back chunk L % CPR of row 64 / CPR * i + L / CPR (the wave's own writes:
     // LDS accesses of one wave complete in order).
     __builtin_amdgcn_wave_barrier();
@@ -1022,7 +1023,7 @@ static int launch_prefill(void* out, const void* q, int64_t q_tok_stride, const 
                           int max_seqlen, int max_context_len, int num_heads, int num_kv_heads,
                           int head_dim, int block_size, int dtype, float scale,
                           ndl_stream_t stream) {
-  if (dtype != NDL_DTYPE_BF16) return NDL_ERR_UNSUPPORTED;
+  if (!dtype_supported(dtype)) return NDL_ERR_UNSUPPORTED;
   if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
     return NDL_ERR_INVALID_ARG;
@@ -1079,11 +1080,17 @@ static int launch_prefill(void* out, const void* q, int64_t q_tok_stride, const 
   a.num_seqs = num_seqs;
   a.persistent = num_seqs <= kPrefListSeqs && qtiles <= kPrefListLevels &&
                  gx * (int64_t)num_seqs * qtiles < ((int64_t)1 << 31);
-  const void* fn = head_dim == 128
-                       ? (rope ? (const void*)varlen_prefill_kernel<128, 6, true>
-                               : (const void*)varlen_prefill_kernel<128, 6, false>)
-                       : (rope ? (const void*)varlen_prefill_kernel<64, 8, true>
-                               : (const void*)varlen_prefill_kernel<64, 8, false>);
+  // [f16][head_dim 128][rope]
+  const void* const fns[2][2][2] = {
+      {{(const void*)varlen_prefill_kernel<64, 8, false, false>,
+        (const void*)varlen_prefill_kernel<64, 8, true, false>},
+       {(const void*)varlen_prefill_kernel<128, 6, false, false>,
+        (const void*)varlen_prefill_kernel<128, 6, true, false>}},
+      {{(const void*)varlen_prefill_kernel<64, 8, false, true>,
+        (const void*)varlen_prefill_kernel<64, 8, true, true>},
+       {(const void*)varlen_prefill_kernel<128, 6, false, true>,
+        (const void*)varlen_prefill_kernel<128, 6, true, true>}}};
+  const void* fn = fns[dtype_is_f16(dtype) ? 1 : 0][head_dim == 128 ? 1 : 0][rope ? 1 : 0];
   dim3 grid((unsigned)gx, (unsigned)num_seqs, (unsigned)qtiles);
   if (a.persistent) {
     const int64_t slots = resident_workgroups(fn, 64 * waves);

@@ -124,14 +124,13 @@ def rope_kv_append(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor,
 
     Same result as _apply_rope (attention.py:88, :277-288) followed by the append
     of attention.py:141-154 (cu_seqlens=None) or _write_kv (:204-246), bit for bit.
-    q [T, H, D], k/v [T, Hkv, D], cos/sin [T, D] in the cache dtype (bf16).
+    q [T, H, D], k/v [T, Hkv, D], cos/sin [T, D] in the cache dtype (bf16 or fp16).
     q=None rotates and appends k (and appends v) only, and returns None: the form that
     precedes rope_varlen_prefill, which rotates q itself.
     """
     _check_cache(kv_cache)
     dev = kv_cache.device
     _, num_blocks, hkv, bs, d = kv_cache.shape
-    _require(kv_cache.dtype == torch.bfloat16, "rope_kv_append supports bfloat16 only", TypeError)
     for name, x in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
         _require(x is None or x.dtype == kv_cache.dtype, f"{name} dtype must match kv_cache",
                  TypeError)

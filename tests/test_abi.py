@@ -89,12 +89,14 @@ def test_rejections_before_any_launch(lib):
     rc = lib.ndl_paged_decode(None, None, 512, None, 1, None, 1, 1, None, 1, 4, 1, 128, 16, 0,
                               1.0, 24, None, 0, None)
     assert rc == -1
-    # rope_kv_append: fp16, a head_dim not a multiple of 16, null inputs
+    # rope_kv_append: an unknown dtype, a head_dim not a multiple of 16, null inputs (fp16
+    # passes the dtype check and fails on them)
     def rope(dtype=0, d=128, t=1, q=None):
         return lib.ndl_rope_kv_append(None, q, 4 * d, None, d, None, d, None, None, d,
                                       None, 1, 4, 1, 16, d, dtype, None, 1, 1, None, None, 1, t,
                                       None)
-    assert rope(dtype=1) == -2
+    assert rope(dtype=7) == -2
+    assert rope(dtype=1) == -1
     assert rope(d=72) == -2
     assert rope(t=0) == 0
     assert rope() == -1
@@ -105,7 +107,7 @@ def test_rejections_before_any_launch(lib):
                                            1, None, None, 1, 1, 1, 0, 4, 1, 128, 16, dtype, 1.0,
                                            None)
     assert rope_prefill() == -1
-    assert rope_prefill(cos=1 << 20, dtype=1) == -2
+    assert rope_prefill(cos=1 << 20, dtype=7) == -2
     assert rope_prefill(cos=1 << 20, cs=100) == -1
     # the allocation-free decode: a shape whose partials exceed the static array is refused
     # after the argument checks and before any device call (1000 sequences x 1000 blocks at
