@@ -298,15 +298,17 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
 
   // K (in row layout, staged through LDS) and V of the tile at block id blk.  An invalid
   // id reads block 0 (always mapped) and marks the tile bad.
-  auto load_tile_blk = [&](int64_t blk, Tile& t) {
+  // live = false: a placeholder load of the same instructions whose lanes all read the
+  // block's first bytes (one cache line per instruction), never computed.
+  auto load_tile_blk = [&](int64_t blk, Tile& t, const bool live = true) {
     t.bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
     if (t.bad) blk = 0;
-    const u16* kb = a.kplane + blk * blk_stride + head_off;
-    const u16* vb = a.vplane + blk * blk_stride + head_off;
+    const u16* kb = a.kplane + blk * blk_stride + head_off + (live ? k_off : 0);
+    const u16* vb = a.vplane + blk * blk_stride + head_off + (live ? v_off : 0);
 #pragma unroll
-    for (int s = 0; s < KS; ++s) t.k[s] = ldg16(kb + k_off + RPI * D * s);
+    for (int s = 0; s < KS; ++s) t.k[s] = ldg16(kb + RPI * D * s);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) t.v[i] = load_vrow<D>(vb + v_off + i * D);
+    for (int i = 0; i < 4; ++i) t.v[i] = load_vrow<D>(vb + i * D);
   };
 
   auto segment = [&](const int seq, const int lt0, const int lt1, const int n_tiles,
@@ -372,8 +374,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       // register came from on the loop's first trip), emptying the ring at each tile.
       asm volatile("" ::"v"(bt_lane));
 
-      auto load_tile = [&](int it, Tile& t) {
-        load_tile_blk(__builtin_amdgcn_readlane(bt_lane, it), t);
+      auto load_tile = [&](int it, Tile& t, const bool live = true) {
+        load_tile_blk(__builtin_amdgcn_readlane(bt_lane, it), t, live);
       };
 
       auto compute_tile = [&](int it, Tile& t) {
@@ -458,16 +460,47 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       };
 
       // NBUF-deep ring: while block `it` computes, blocks it+1 .. it+NBUF-1 are in flight.
+      const int last = ntiles - 1;
       Tile buf[NBUF];
+      if constexpr (NW > 1) {
+        // Per-sequence workgroups (few tiles per wave, latency-bound): every compute in
+        // the loop follows its slot's load; once the next slot would lie past the window's
+        // last tile, the tiles still loaded compute at that point and the walk leaves the
+        // window.  (A load skipped on some path into a compute makes the compiler's wait
+        // before each tile, which must hold on every path, "all loads", so the tile in
+        // flight behind it is waited for too.)  Prologue slots past the end of a window
+        // shorter than the ring are placeholder loads.
 #pragma unroll
-      for (int u = 0; u < NBUF - 1; ++u)
-        if (u < ntiles) load_tile(u, buf[u]);
-      for (int it = 0; it < ntiles; it += NBUF) {
+        for (int u = 0; u < NBUF - 1; ++u) load_tile(u < last ? u : last, buf[u], u <= last);
+        bool drained = false;
+        for (int it = 0; !drained; it += NBUF) {
 #pragma unroll
-        for (int u = 0; u < NBUF; ++u) {
-          const int nxt = it + u + NBUF - 1;
-          if (nxt < ntiles) load_tile(nxt, buf[(u + NBUF - 1) % NBUF]);
-          if (it + u < ntiles) compute_tile(it + u, buf[u]);
+          for (int u = 0; u < NBUF; ++u) {
+            const int nxt = it + u + NBUF - 1;
+            if (nxt > last) {   // tiles it+u .. last are loaded, in slots u, u+1, ..
+#pragma unroll
+              for (int d = 0; d < NBUF - 1; ++d)
+                if (it + u + d <= last) compute_tile(it + u + d, buf[(u + d) % NBUF]);
+              drained = true;
+              break;
+            }
+            load_tile(nxt, buf[(u + NBUF - 1) % NBUF]);
+            compute_tile(it + u, buf[u]);
+          }
+        }
+      } else {
+        // The stream split (many waves per SIMD hide the latency; a second copy of the
+        // tile code for the ring's tail would exceed its register budget).
+#pragma unroll
+        for (int u = 0; u < NBUF - 1; ++u)
+          if (u <= last) load_tile(u, buf[u]);
+        for (int it = 0; it < ntiles; it += NBUF) {
+#pragma unroll
+          for (int u = 0; u < NBUF; ++u) {
+            const int nxt = it + u + NBUF - 1;
+            if (nxt <= last) load_tile(nxt, buf[(u + NBUF - 1) % NBUF]);
+            if (it + u <= last) compute_tile(it + u, buf[u]);
+          }
         }
       }
     }
