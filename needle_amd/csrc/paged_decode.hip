@@ -47,11 +47,13 @@ namespace ndl {
 
 // The fewest tiles a wave of the automatic split takes.
 constexpr int kDecodeMinChunk = 2;
-// Waves per workgroup of the per-sequence split (as many as one CU holds at the
-// kernel's register use: 16 at head_dim 64, 8 at 128), and the most tiles per wave for
-// which the automatic choice takes it.
-template <int D> constexpr int seq_split_waves() { return D == 64 ? 16 : 8; }
-constexpr int kSeqSplitMaxTiles = 16;
+// Waves per workgroup of the per-sequence split, and the most tiles per wave for which
+// the automatic choice takes it (a table of up to 256 columns at head_dim 64, 128 at
+// 128).  Eight waves (two per SIMD) measured faster than sixteen (four per SIMD) at
+// head_dim 64, e.g. the Qwen2-0.5B decode step 6.07 against 7.46 us with cold pools,
+// and faster than four at both head dims.
+template <int D> constexpr int seq_split_waves() { return 8; }
+template <int D> constexpr int seq_split_max_tiles() { return D == 64 ? 32 : 16; }
 
 template <int D> struct VRow;
 template <> struct VRow<128> { using T = u32x4; };  // 8 bf16 per lane per token
@@ -859,7 +861,7 @@ struct DecodeLayout {
 // (kv head, sequence).  partition_tokens > 0 (a multiple of 16): the stream split with
 // that many tokens per wave.  0: the per-sequence workgroups when all of them are
 // resident at once and a sequence of the full table width needs at most
-// kSeqSplitMaxTiles tiles per wave; otherwise the stream split over as many waves as
+// seq_split_max_tiles() tiles per wave; otherwise the stream split over as many waves as
 // can be resident at once, shared by the kv heads, so that every wave that has tiles
 // runs from the start (a device that cannot be queried counts as 2048 waves); each
 // takes ceil(T / waves) tiles of its stream.
@@ -876,7 +878,8 @@ inline int decode_layout(int num_seqs, int num_heads, int num_kv_heads, int head
         head_dim == 128 ? seq_split_kernel_fn<128>() : seq_split_kernel_fn<64>(), 64 * nw);
     if (resident <= 0) resident = 2048;
     if ((int64_t)num_kv_heads * num_seqs * nw <= resident &&
-        (max_blocks + nw - 1) / nw <= kSeqSplitMaxTiles)
+        (max_blocks + nw - 1) / nw <=
+            (head_dim == 128 ? seq_split_max_tiles<128>() : seq_split_max_tiles<64>()))
       lay->seq_split = nw;
   }
   if (lay->seq_split) {  // no partials leave the workgroup
