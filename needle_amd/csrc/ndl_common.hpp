@@ -132,6 +132,17 @@ __device__ __forceinline__ void rope8(const u32x4& lo, const u32x4& hi, const u3
   }
 }
 
+// Block sizes the attention kernels take: powers of two from 16 to 1024 tokens, each block
+// read as 16-token tiles.  log2(block_size / 16), or -1 for any other size.
+constexpr int kMaxBlockSize = 1024;
+inline int block_tile_shift(int block_size) {
+  if (block_size < 16 || block_size > kMaxBlockSize || (block_size & (block_size - 1)))
+    return -1;
+  int s = 0;
+  while ((16 << s) < block_size) ++s;
+  return s;
+}
+
 // The element format of an ABI dtype code (false: bf16, true: fp16); false for others.
 inline bool dtype_is_f16(int dtype) { return dtype == NDL_DTYPE_F16; }
 inline bool dtype_supported(int dtype) {

@@ -78,6 +78,9 @@ struct DecodeArgs {
   const int32_t* block_table;
   int64_t bt_row_stride;
   int max_blocks;
+  // log2(block_size / 16): a block (table column) holds 1 << tile_shift tiles of 16 tokens;
+  // tile t of a sequence is rows 16 (t mod 2^shift) .. + 16 of its column t >> shift.
+  int tile_shift;
   const int32_t* context_lens;
   int num_heads;
   int group;
@@ -102,7 +105,8 @@ struct DecodeArgs {
 
 __device__ __forceinline__ int64_t attended_len(const DecodeArgs& a, int seq) {
   int64_t L = (int64_t)a.context_lens[seq] + 1;  // attention.py:299
-  const int64_t cap = (int64_t)a.max_blocks * 16;  // a table row holds at most W blocks
+  // a table row holds at most W blocks of 16 << tile_shift tokens
+  const int64_t cap = (int64_t)a.max_blocks << (4 + a.tile_shift);
   return L < cap ? L : cap;
 }
 
@@ -206,8 +210,9 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
   const bool head_ok = c < a.group;
   const int head = kvh * a.group + c;
 
-  const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
-  const int64_t head_off = (int64_t)kvh * 16 * D;
+  const int tshift = a.tile_shift, tmask = (1 << tshift) - 1;
+  const int64_t blk_stride = (int64_t)a.num_kv_heads * (16 << tshift) * D;
+  const int64_t head_off = (int64_t)kvh * (16 << tshift) * D;
   // K is fetched in row layout (each load instruction reads RPI whole rows, 1 KiB
   // contiguous), staged in LDS and read back in the MFMA A-operand layout.
   constexpr int CPR = D / 8;      // 16-byte chunks per row
@@ -300,13 +305,15 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
 
   // K (in row layout, staged through LDS) and V of the tile at block id blk.  An invalid
   // id reads block 0 (always mapped) and marks the tile bad.
-  // live = false: a placeholder load of the same instructions whose lanes all read the
-  // block's first bytes (one cache line per instruction), never computed.
-  auto load_tile_blk = [&](int64_t blk, Tile& t, const bool live = true) {
+  // Tile `sub` (16 rows) of block blk.  live = false: a placeholder load of the same
+  // instructions whose lanes all read the tile's first bytes (one cache line per
+  // instruction), never computed.
+  auto load_tile_blk = [&](int64_t blk, int sub, Tile& t, const bool live = true) {
     t.bad = blk < 0 || blk >= a.num_blocks;  // wave-uniform
     if (t.bad) blk = 0;
-    const u16* kb = a.kplane + blk * blk_stride + head_off + (live ? k_off : 0);
-    const u16* vb = a.vplane + blk * blk_stride + head_off + (live ? v_off : 0);
+    const int64_t tile_off = blk * blk_stride + head_off + (int64_t)sub * 16 * D;
+    const u16* kb = a.kplane + tile_off + (live ? k_off : 0);
+    const u16* vb = a.vplane + tile_off + (live ? v_off : 0);
 #pragma unroll
     for (int s = 0; s < KS; ++s) t.k[s] = ldg16(kb + RPI * D * s);
 #pragma unroll
@@ -323,20 +330,28 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
 
     // Fused append (attention.py:141-154 before :156-159): the new token of the step sits
-    // at position context_lens[seq], row context_lens[seq] % 16 of the sequence's last tile
-    // (the append's column min(p / 16, W - 1) is the last attended tile, also when the
-    // table row clamps).  The wave that owns that tile writes the row into the cache and
-    // uses it in place of the row it loaded; no other wave reads the tile.  Each lane loads
-    // the pieces of the new rows it holds in the tile layouts: chunk k_chunk of K, head_dim
-    // DPL*c .. of V.  The row is stored while the segment's first tile computes: stores
-    // count in the in-order memory counter, and stored there, only loads issued after it
-    // (a tile later) wait for it.
-    // wave-uniform: this wave attends the sequence's last tile
-    const bool app = APP && lt1 == n_tiles && (n_tiles - 1 - lt0) % stride == 0;
+    // at position p = context_lens[seq], row p % bs of table column min(p / bs, W - 1)
+    // (:144-146), i.e. row p % 16 of tile app_tile, an attended tile (the last one unless
+    // the table row clamps with blocks of more than 16 tokens).  The wave that owns that
+    // tile writes the row into the cache and uses it in place of the row it loaded; no
+    // other wave reads the tile.  Each lane loads the pieces of the new rows it holds in
+    // the tile layouts: chunk k_chunk of K, head_dim DPL*c .. of V.  The row is stored
+    // while the segment's first tile computes: stores count in the in-order memory
+    // counter, and stored there, only loads issued after it (a tile later) wait for it.
+    int app_tile = -1;
+    if constexpr (APP) {
+      const int p = a.context_lens[seq];   // >= 0: the sequence attends tiles
+      const int pc = p >> (4 + tshift);
+      app_tile = ((pc < a.max_blocks - 1 ? pc : a.max_blocks - 1) << tshift) | ((p >> 4) & tmask);
+    }
+    // wave-uniform: this wave attends the appended row's tile
+    const bool app = APP && app_tile >= lt0 && app_tile < lt1 && (app_tile - lt0) % stride == 0;
     const int r_new = app ? a.context_lens[seq] & 15 : 0;
+    // the row's offset in its block's (kv head) slice
+    const int64_t app_row_off = (int64_t)(((app_tile & tmask) << 4) + r_new) * D;
     u32x4 k_app = {0u, 0u, 0u, 0u};
     VT v_app = {};
-    int64_t app_blk = -1;   // the last tile's block (its table column), if valid
+    int64_t app_blk = -1;   // the appended row's block (its table column), if valid
     if (app) {
       const u16* krow = a.k_new + (int64_t)seq * a.k_new_stride + (int64_t)kvh * D;
       k_app = ld16(krow + 8 * k_chunk);
@@ -355,7 +370,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       }
       v_app = load_vrow<D>(a.v_new + (int64_t)seq * a.v_new_stride + (int64_t)kvh * D + DPL * c);
       if constexpr (kStoreRow) {
-        const int64_t b = a.block_table[(int64_t)seq * a.bt_row_stride + n_tiles - 1];
+        const int64_t b = a.block_table[(int64_t)seq * a.bt_row_stride + (app_tile >> tshift)];
         app_blk = b >= 0 && b < a.num_blocks ? b : -1;
       }
     }
@@ -370,21 +385,22 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
       const int left = (lt1 - w0 + stride - 1) / stride;          // tiles from w0 on
       const int ntiles = left < 64 ? left : 64;
       const int bt_lane = (first_bt != nullptr && w0 == lt0) ? *first_bt
-                          : lane < ntiles ? bt_row[w0 + stride * lane] : 0;
+                          : lane < ntiles ? bt_row[(w0 + stride * lane) >> tshift] : 0;
       // The window's ids are waited for here, once: a use inside the tile ring below would
       // otherwise wait for every load in flight (the compiler cannot tell which load the
       // register came from on the loop's first trip), emptying the ring at each tile.
       asm volatile("" ::"v"(bt_lane));
 
       auto load_tile = [&](int it, Tile& t, const bool live = true) {
-        load_tile_blk(__builtin_amdgcn_readlane(bt_lane, it), t, live);
+        load_tile_blk(__builtin_amdgcn_readlane(bt_lane, it), (w0 + stride * it) & tmask, t,
+                      live);
       };
 
       auto compute_tile = [&](int it, Tile& t) {
         const int tix = w0 + stride * it;   // the tile's index in the sequence
         if (kStoreRow && app && tix == lt0 && app_blk >= 0) {   // the segment's first tile
-          u16* const kb = const_cast<u16*>(a.kplane) + app_blk * blk_stride + head_off + r_new * D;
-          u16* const vb = const_cast<u16*>(a.vplane) + app_blk * blk_stride + head_off + r_new * D;
+          u16* const kb = const_cast<u16*>(a.kplane) + app_blk * blk_stride + head_off + app_row_off;
+          u16* const vb = const_cast<u16*>(a.vplane) + app_blk * blk_stride + head_off + app_row_off;
           if (k_row == r_new % RPI) st16(kb + 8 * k_chunk, k_app);
           if (j == (r_new >> 2)) {
             if constexpr (D == 128)
@@ -393,7 +409,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
               *reinterpret_cast<VT*>(vb + DPL * c) = v_app;
           }
         }
-        if (app && tix == n_tiles - 1 && !t.bad) {   // the appended token's tile
+        if (app && tix == app_tile && !t.bad) {   // the appended token's tile
 #pragma unroll
           for (int s = 0; s < KS; ++s)
             if (RPI * s + k_row == r_new) t.k[s] = k_app;
@@ -582,7 +598,7 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
     // Wave w takes tiles w, w + NW, w + 2 NW, .. of the sequence.  Their block ids (one
     // column per lane) do not depend on the context length, so they load alongside it.
     const int seq = sw;
-    const int col = wv + NW * lane;
+    const int col = (wv + NW * lane) >> tshift;   // the table column of this lane's tile
     const int first_bt =
         a.block_table[(int64_t)seq * a.bt_row_stride + (col < a.max_blocks ? col : a.max_blocks - 1)];
     const int nt = seq_tiles(a, seq);
@@ -659,13 +675,15 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
   const int kvh = head / a.group, hc = head - kvh * a.group;
   // The decode step's new K/V row (ndl_paged_decode_append): the attention kernel attended
   // it from registers; the first query head's wave of each (kv head, sequence) stores it,
-  // with the separate append's rule (attention.py:141-154): column min(ctx / 16, W - 1),
-  // row ctx % 16, nothing for a negative context or an invalid block id.
+  // with the separate append's rule (attention.py:141-154): column min(ctx / bs, W - 1),
+  // row ctx % bs, nothing for a negative context or an invalid block id.
   if (a.k_new != nullptr && hc == 0) {
     constexpr int CH = D / 8;   // 16-byte chunks per row; lanes < CH: K, < 2 CH: V
     const int ctx = a.context_lens[seq];
     if (ctx >= 0 && lane < 2 * CH) {
-      const int col = ctx / 16 < a.max_blocks - 1 ? ctx / 16 : a.max_blocks - 1;
+      const int bshift = 4 + a.tile_shift;   // log2(block_size)
+      const int pc = ctx >> bshift;
+      const int col = pc < a.max_blocks - 1 ? pc : a.max_blocks - 1;
       const int64_t b = a.block_table[(int64_t)seq * a.bt_row_stride + col];
       if (b >= 0 && b < a.num_blocks) {
         const bool is_v = lane >= CH;
@@ -673,7 +691,8 @@ __global__ __launch_bounds__(64) void paged_decode_merge_kernel(DecodeArgs a) {
         const u16* src_row = (is_v ? a.v_new + (int64_t)seq * a.v_new_stride
                                    : a.k_new + (int64_t)seq * a.k_new_stride) + (int64_t)kvh * D;
         u16* row = const_cast<u16*>(is_v ? a.vplane : a.kplane) +
-                   (b * a.num_kv_heads + kvh) * (int64_t)(16 * D) + (ctx & 15) * D + 8 * ch;
+                   ((b * a.num_kv_heads + kvh) << bshift) * D +
+                   (int64_t)(ctx & ((1 << bshift) - 1)) * D + 8 * ch;
         u32x4 val = ld16(src_row + 8 * ch);
         if (!is_v && a.rope_cos != nullptr) {   // the key row rotated as the attention did
           constexpr int HC = CH / 2;
@@ -865,8 +884,9 @@ struct DecodeLayout {
 // can be resident at once, shared by the kv heads, so that every wave that has tiles
 // runs from the start (a device that cannot be queried counts as 2048 waves); each
 // takes ceil(T / waves) tiles of its stream.
+// max_tiles: 16-token tiles of a full table row (its width times block_size / 16).
 inline int decode_layout(int num_seqs, int num_heads, int num_kv_heads, int head_dim,
-                         int max_blocks, int partition_tokens, DecodeLayout* lay) {
+                         int64_t max_tiles, int partition_tokens, DecodeLayout* lay) {
   lay->seq_split = 0;
   const int nw = head_dim == 128 ? seq_split_waves<128>() : seq_split_waves<64>();
   if (partition_tokens == -1) {
@@ -878,7 +898,7 @@ inline int decode_layout(int num_seqs, int num_heads, int num_kv_heads, int head
         head_dim == 128 ? seq_split_kernel_fn<128>() : seq_split_kernel_fn<64>(), 64 * nw);
     if (resident <= 0) resident = 2048;
     if ((int64_t)num_kv_heads * num_seqs * nw <= resident &&
-        (max_blocks + nw - 1) / nw <=
+        (max_tiles + nw - 1) / nw <=
             (head_dim == 128 ? seq_split_max_tiles<128>() : seq_split_max_tiles<64>()))
       lay->seq_split = nw;
   }
@@ -894,7 +914,7 @@ inline int decode_layout(int num_seqs, int num_heads, int num_kv_heads, int head
     if (partition_tokens % 16 != 0) return NDL_ERR_INVALID_ARG;
     lay->chunk = partition_tokens / 16;
     // stream slots: every sequence's tiles and its kStreamPad empty slots
-    lay->waves = ((int64_t)num_seqs * (max_blocks + kStreamPad) + lay->chunk - 1) / lay->chunk;
+    lay->waves = ((int64_t)num_seqs * (max_tiles + kStreamPad) + lay->chunk - 1) / lay->chunk;
   } else {
     int64_t resident = decode_resident_waves(
         head_dim == 128 ? decode_kernel_fn<128>(decode_pipeline_depth())
@@ -919,12 +939,13 @@ extern "C" size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, 
                                                    int head_dim, int max_blocks_per_seq,
                                                    int block_size, int partition_tokens) {
   using namespace ndl;
+  const int tshift = block_tile_shift(block_size);
   if (num_seqs <= 0 || num_heads <= 0 || num_kv_heads <= 0 || num_heads % num_kv_heads != 0 ||
-      head_dim <= 0 || max_blocks_per_seq <= 0 || block_size != 16)
+      head_dim <= 0 || max_blocks_per_seq <= 0 || tshift < 0)
     return 0;
   DecodeLayout lay;
-  if (decode_layout(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
-                    partition_tokens, &lay) != NDL_OK)
+  if (decode_layout(num_seqs, num_heads, num_kv_heads, head_dim,
+                    (int64_t)max_blocks_per_seq << tshift, partition_tokens, &lay) != NDL_OK)
     return 0;
   return lay.bytes;
 }
@@ -987,7 +1008,8 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
                          bool static_scratch = false, const void* rope_cos = nullptr,
                          const void* rope_sin = nullptr, int64_t rope_stride = 0) {
   if (!dtype_supported(dtype)) return NDL_ERR_UNSUPPORTED;
-  if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
+  const int tshift = block_tile_shift(block_size);
+  if (tshift < 0 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
     return NDL_ERR_INVALID_ARG;
   const int group = num_heads / num_kv_heads;
@@ -1003,13 +1025,14 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   if (q_tok_stride & 7) return NDL_ERR_INVALID_ARG;
   if (num_seqs > 65535) return NDL_ERR_UNSUPPORTED;
   DecodeLayout lay;
-  const int rc0 = decode_layout(num_seqs, num_heads, num_kv_heads, head_dim, max_blocks_per_seq,
+  const int64_t max_tiles = (int64_t)max_blocks_per_seq << tshift;
+  if (max_tiles > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
+  const int rc0 = decode_layout(num_seqs, num_heads, num_kv_heads, head_dim, max_tiles,
                                 partition_tokens, &lay);
   if (rc0 != NDL_OK) return rc0;
   // Segments one sequence can span: its tiles over the chunk, plus the partial ends
   // (the automatic split keeps waves <= kMergeMaxParts - 2).
-  if (!lay.seq_split && lay.chunk > 0 &&
-      (int64_t)max_blocks_per_seq / lay.chunk + 2 > kMergeMaxParts)
+  if (!lay.seq_split && lay.chunk > 0 && max_tiles / lay.chunk + 2 > kMergeMaxParts)
     return NDL_ERR_UNSUPPORTED;
   const int64_t grid_waves = lay.seq_split ? (int64_t)num_seqs * num_kv_heads
                                            : lay.waves * num_kv_heads;
@@ -1028,12 +1051,13 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   a.q = (const u16*)q;
   a.q_tok_stride = q_tok_stride;
   a.kplane = (const u16*)kv_cache;
-  a.vplane = a.kplane + num_blocks * num_kv_heads * (int64_t)16 * head_dim;
+  a.vplane = a.kplane + num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
   a.num_blocks = num_blocks;
   a.num_kv_heads = num_kv_heads;
   a.block_table = block_table;
   a.bt_row_stride = bt_row_stride;
   a.max_blocks = max_blocks_per_seq;
+  a.tile_shift = tshift;
   a.context_lens = context_lens;
   a.num_heads = num_heads;
   a.group = group;

@@ -68,7 +68,10 @@ struct PrefillArgs {
   int num_kv_heads;
   const int32_t* block_table;
   int64_t bt_row_stride;
-  int max_blocks;
+  // Keys are read in 16-token tiles: a block (table column) holds 1 << tile_shift of them
+  // (log2(block_size / 16)), so a table row of W columns holds max_tiles = W << tile_shift.
+  int tile_shift;
+  int max_tiles;
   const int32_t* cu_seqlens;
   const int32_t* context_lens;
   int num_heads;
@@ -265,20 +268,32 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     // Position of this wave's last query row (-1: the wave has no rows).
     const int qpos_last = wave_active ? ctx + (wrow0 + kPrefRows <= n ? wrow0 + kPrefRows : n) - 1 : -1;
 
-    const int64_t blk_stride = (int64_t)a.num_kv_heads * 16 * D;
+    const int tshift = a.tile_shift, tmask = (1 << tshift) - 1;
     const int32_t* bt_row = a.block_table + (int64_t)seq * a.bt_row_stride;
     // Block ids are int32; every id in [0, nb32) is a valid block.
     const uint32_t nb32 = a.num_blocks > 0x7fffffff ? 0x80000000u : (uint32_t)a.num_blocks;
+    // Tile `sub` of block b, kv head kvh, starts at plane + kvh * bs * D + u * 16 * D with
+    // u = b * Hkv * 2^shift + sub (the tile's index in units of 16 rows; u * 16 * D is
+    // within the plane, so u fits 32 bits).
+    const uint32_t units_per_blk = (uint32_t)a.num_kv_heads << tshift;
 
-    // Block ids come from a 64-entry window of the table row held one per lane and are
-    // read with readlane (uniform).  The first window goes out with the Q loads below
-    // and one wait covers both; a later refill waits for every outstanding load (a
-    // vector-memory wait cannot single one out); it happens once per 64 blocks.
+    // The tiles' block ids come from a 64-tile window of the table row, one tile per lane
+    // (lane l: tile win0 + l, table column (win0 + l) >> shift), held as unit indices u
+    // (an invalid id as block 0, with its lane's bit set in win_badm) and read with
+    // readlane (uniform).  The first window goes out with the Q loads below and one wait
+    // covers both; a later refill waits for every outstanding load (a vector-memory wait
+    // cannot single one out); it happens once per 64 tiles.
     int win0 = 0;
     int btw = 0;
+    uint64_t win_badm = 0;
+    auto to_unit = [&](int raw, int t) {
+      return (int)(((uint32_t)raw < nb32 ? (uint32_t)raw : 0u) * units_per_blk +
+                   (uint32_t)(t & tmask));
+    };
     if (!pre && wave == 0) {
       const int l = fresh_lane();
-      lds_dma4(bt_row, 4u * (uint32_t)(l < a.max_blocks ? l : a.max_blocks - 1), lds_addr(s_btw));
+      lds_dma4(bt_row, 4u * (uint32_t)((l < a.max_tiles ? l : a.max_tiles - 1) >> tshift),
+               lds_addr(s_btw));
       vm_wait<0>();
     }
 
@@ -298,7 +313,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     //     per row): lane L -> row L/4, chunk 4 e + L%4.
     static_assert((PIECES / 2) % IPW == 0, "load distribution");
     const int ld_plane = wave >> 2, ld_blk = (wave >> 1) & 1, ld_half = wave & 1;
-    const u16* ld_head = (ld_plane ? a.vplane : a.kplane) + (int64_t)kvh * 16 * D;
+    const u16* ld_head = (ld_plane ? a.vplane : a.kplane) + ((int64_t)kvh << tshift) * 16 * D;
     uint32_t ld_off[IPW];
 #pragma unroll
     for (int e = 0; e < IPW; ++e) {
@@ -316,7 +331,7 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     const uint32_t ld_lds =
         (ld_plane ? lds_v0 : lds_k0) + (ld_blk * (PIECES / 2) + ld_half * IPW) * 1024;
 
-    auto clamp_col = [&](int col) { return col > a.max_blocks - 1 ? a.max_blocks - 1 : col; };
+    auto clamp_col = [&](int col) { return col > a.max_tiles - 1 ? a.max_tiles - 1 : col; };
     // bit 2*stage + b: block b of that stage's step is not a valid id.  Every wave keeps
     // its own copy (all waves walk the same table window).
     uint32_t badbits = 0;
@@ -325,24 +340,23 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     // direct loads of it.  An invalid block id reads block 0 instead (always mapped);
     // rows past the range read whatever the table maps them to.  The softmax masks both.
     // A window of the table with no invalid id (the normal case) sets no bits.
-    bool win_bad = false;
     auto stage_in = [&](int step, int stage) {
       const int c0 = clamp_col(2 * step), c1 = clamp_col(2 * step + 1);  // same 64-window
       if (c0 < win0 || c0 >= win0 + 64) {
         win0 = c0 & ~63;
         const int l = fresh_lane();
-        btw = win0 + l < a.max_blocks ? bt_row[win0 + l] : 0;
+        const int raw = win0 + l < a.max_tiles ? bt_row[(win0 + l) >> tshift] : 0;
         vm_wait<0>();
-        win_bad = __builtin_amdgcn_ballot_w64(win0 + lane < a.max_blocks &&
-                                              (uint32_t)btw >= nb32) != 0;
+        win_badm = __builtin_amdgcn_ballot_w64(win0 + lane < a.max_tiles &&
+                                               (uint32_t)raw >= nb32);
+        btw = to_unit(raw, win0 + l);
       }
       badbits &= ~(3u << (2 * stage));
-      const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane(btw, c0 - win0);
-      const uint32_t b1 = (uint32_t)__builtin_amdgcn_readlane(btw, c1 - win0);
-      if (win_bad)
-        badbits |= ((b0 >= nb32 ? 1u : 0u) | (b1 >= nb32 ? 2u : 0u)) << (2 * stage);
-      const uint32_t b = ld_blk ? b1 : b0;
-      const u16* base = ld_head + (int64_t)(b < nb32 ? b : 0u) * blk_stride;
+      if (win_badm)
+        badbits |= ((uint32_t)((win_badm >> (c0 - win0)) & 1u) |
+                    ((uint32_t)((win_badm >> (c1 - win0)) & 1u) << 1)) << (2 * stage);
+      const uint32_t u = (uint32_t)__builtin_amdgcn_readlane(btw, (ld_blk ? c1 : c0) - win0);
+      const u16* base = ld_head + (int64_t)u * 16 * D;
       const uint32_t lds = ld_lds + (uint32_t)stage * (kPrefKeys * D * 2);
 #pragma unroll
       for (int e = 0; e < IPW; ++e)
@@ -623,8 +637,9 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
     lds_barrier();
     {
       const int l = fresh_lane();
-      btw = l < a.max_blocks ? s_btw[l] : 0;
-      win_bad = __builtin_amdgcn_ballot_w64(l < a.max_blocks && (uint32_t)btw >= nb32) != 0;
+      const int raw = l < a.max_tiles ? s_btw[l] : 0;
+      win_badm = __builtin_amdgcn_ballot_w64(l < a.max_tiles && (uint32_t)raw >= nb32);
+      btw = to_unit(raw, l);
     }
     stage_in(0, 0);
     if (nsteps > 1) stage_in(1, 1);
@@ -695,7 +710,8 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       if (wave == 0) {
         const int l = fresh_lane();
         lds_dma4(a.block_table + (int64_t)nx.seq * a.bt_row_stride,
-                 4u * (uint32_t)(l < a.max_blocks ? l : a.max_blocks - 1), lds_addr(s_btw));
+                 4u * (uint32_t)((l < a.max_tiles ? l : a.max_tiles - 1) >> tshift),
+                 lds_addr(s_btw));
       }
       btw_next = true;
     }
@@ -723,28 +739,27 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
       auto stage_fast = [&](int x, int sl) {
         if (x >= nsteps) return;
         const int c0 = 2 * x;
-        if (c0 >= win0 + 64 || win_bad || c0 + 1 >= a.max_blocks) {
+        if (c0 >= win0 + 64 || win_badm || c0 + 1 >= a.max_tiles) {
           stage_in(x, sl);
           return;
         }
-        const uint32_t b = (uint32_t)__builtin_amdgcn_readlane(btw, c0 + ld_blk - win0);
-        const u16* base = ld_head + (int64_t)b * blk_stride;
+        const uint32_t u = (uint32_t)__builtin_amdgcn_readlane(btw, c0 + ld_blk - win0);
+        const u16* base = ld_head + (int64_t)u * 16 * D;
         const uint32_t lds = ld_lds + (uint32_t)sl * (kPrefKeys * D * 2);
 #pragma unroll
         for (int e = 0; e < IPW; ++e)
           lds_dma16(base, ld_off[e], lds + 1024 * e);
       };
-      // Byte offset of a block in a plane: Hkv * 16 * D * 2 bytes per block fits 32 bits.
-      const uint32_t blk_bytes = (uint32_t)(blk_stride * 2);
+      constexpr uint32_t unit_bytes = 16 * D * 2;   // one 16-row tile of one kv head
       while (step < lim && badbits == 0) {
         // Fast trips: every per-trip check of the trip below holds for the whole run, so it
         // is tested once: both steps staged (step + NS - 2, step + NS - 1) exist and their
-        // four table columns lie inside the current window and the table row (no clamp);
+        // four tiles lie inside the current window and the table row (no clamp);
         // the window has no invalid id (badbits stays 0); step + 2 is a full step (no V
         // rows to clear); the ring is in full flow (a constant load wait).  What is left
         // per trip is the barrier, two block look-ups and their loads.
-        if (!win_bad) {
-          const int wcols = win0 + 64 < a.max_blocks ? win0 + 64 : a.max_blocks;
+        if (!win_badm) {
+          const int wcols = win0 + 64 < a.max_tiles ? win0 + 64 : a.max_tiles;
           int end = lim;
           if (nsteps - NS + 1 < end) end = nsteps - NS + 1;            // step + NS - 1 exists
           if (kv_end / kPrefKeys - 2 < end) end = kv_end / kPrefKeys - 2;   // step + 2 full
@@ -760,13 +775,13 @@ __global__ __launch_bounds__(64 * kPrefWaves) void varlen_prefill_kernel(Prefill
             v_reads(stage, vop);
             st1 = qk(ka);
             {
-              // This wave's block of steps step + NS - 2 and step + NS - 1: table columns
-              // ci and ci + 2 of the window.
+              // This wave's tile of steps step + NS - 2 and step + NS - 1: tiles ci and
+              // ci + 2 of the window.
               const int ci = 2 * (step + NS - 2) + ld_blk - win0;
               const uint32_t b0 = (uint32_t)__builtin_amdgcn_readlane(btw, ci);
               const uint32_t b1 = (uint32_t)__builtin_amdgcn_readlane(btw, ci + 2);
-              const u16* base0 = (const u16*)((const char*)ld_head + (uint64_t)b0 * blk_bytes);
-              const u16* base1 = (const u16*)((const char*)ld_head + (uint64_t)b1 * blk_bytes);
+              const u16* base0 = (const u16*)((const char*)ld_head + (uint64_t)b0 * unit_bytes);
+              const u16* base1 = (const u16*)((const char*)ld_head + (uint64_t)b1 * unit_bytes);
               const uint32_t l0 = ld_lds + (uint32_t)slot_after(stage, NS - 2) * (kPrefKeys * D * 2);
               const uint32_t l1 = ld_lds + (uint32_t)slot_after(stage, NS - 1) * (kPrefKeys * D * 2);
 #pragma unroll
@@ -1024,13 +1039,15 @@ static int launch_prefill(void* out, const void* q, int64_t q_tok_stride, const 
                           int head_dim, int block_size, int dtype, float scale,
                           ndl_stream_t stream) {
   if (!dtype_supported(dtype)) return NDL_ERR_UNSUPPORTED;
-  if (block_size != 16 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
+  const int tshift = block_tile_shift(block_size);
+  if (tshift < 0 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
     return NDL_ERR_INVALID_ARG;
   if (num_seqs < 0 || num_tokens < 0 || max_seqlen < 0 || max_context_len < 0 ||
       num_blocks <= 0 || max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq ||
       q_tok_stride < (int64_t)num_heads * head_dim)
     return NDL_ERR_INVALID_ARG;
+  if (((int64_t)max_blocks_per_seq << tshift) > 0x7fffffff) return NDL_ERR_UNSUPPORTED;
   const bool rope = cos != nullptr || sin != nullptr;
   if (rope && (cos == nullptr || sin == nullptr || cs_tok_stride < head_dim ||
                (cs_tok_stride & 7) || (((uintptr_t)cos | (uintptr_t)sin) & 15u)))
@@ -1057,12 +1074,13 @@ static int launch_prefill(void* out, const void* q, int64_t q_tok_stride, const 
   a.q = (const u16*)q;
   a.q_tok_stride = q_tok_stride;
   a.kplane = (const u16*)kv_cache;
-  a.vplane = a.kplane + num_blocks * num_kv_heads * (int64_t)16 * head_dim;
+  a.vplane = a.kplane + num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
   a.num_blocks = num_blocks;
   a.num_kv_heads = num_kv_heads;
   a.block_table = block_table;
   a.bt_row_stride = bt_row_stride;
-  a.max_blocks = max_blocks_per_seq;
+  a.tile_shift = tshift;
+  a.max_tiles = max_blocks_per_seq << tshift;
   a.cu_seqlens = cu_seqlens;
   a.context_lens = context_lens;
   a.num_heads = num_heads;

@@ -66,7 +66,7 @@ def test_decode_workspace_sizing(lib):
     assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 0) == 256
     assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, -2) == 0
     # unsupported block size / partition not a multiple of 16 / heads not a multiple
-    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 32, 256) == 0
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 48, 256) == 0
     assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 16, 100) == 0
     assert lib.ndl_paged_decode_workspace_bytes(2, 32, 6, 128, 64, 16, 0) == 0
 
@@ -79,9 +79,25 @@ def test_rejections_before_any_launch(lib):
     rc = lib.ndl_paged_decode(None, None, 0, None, 1, None, 1, 1, None, 1, 4, 1, 96, 16, 0,
                               1.0, 0, None, 0, None)
     assert rc == -2
-    rc = lib.ndl_paged_decode(None, None, 0, None, 1, None, 1, 1, None, 1, 4, 1, 128, 32, 0,
-                              1.0, 0, None, 0, None)
-    assert rc == -2
+    # block sizes: powers of two from 16 to 1024 pass the size check (and fail here on the
+    # null arguments); others are not built
+    def dec_bs(bs):
+        return lib.ndl_paged_decode(None, None, 0, None, 1, None, 1, 1, None, 1, 4, 1, 128, bs,
+                                    0, 1.0, 0, None, 0, None)
+
+    def pre_bs(bs):
+        return lib.ndl_varlen_prefill(None, None, 4 * 128, None, 1, None, 1, 1, None, None, 1,
+                                      1, 1, 0, 4, 1, 128, bs, 0, 1.0, None)
+    for bs in (16, 32, 64, 128, 256, 1024):
+        assert dec_bs(bs) == -1 and pre_bs(bs) == -1, bs
+    for bs in (0, 8, 24, 48, 2048):
+        assert dec_bs(bs) == -2 and pre_bs(bs) == -2, bs
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 8, 0) == 0
+    # the split is sized in 16-token tiles: 64 columns of 64 tokens = 256 tiles per row,
+    # past the per-sequence split's cap at head_dim 128, so the stream split's workspace
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 64, 0) > 256
+    assert lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 64, 64, 256) == \
+        lib.ndl_paged_decode_workspace_bytes(2, 32, 8, 128, 256, 16, 256)
     rc = lib.ndl_paged_decode(None, None, 0, None, 1, None, 1, 1, None, 1, 40, 2, 128, 16, 0,
                               1.0, 0, None, 0, None)
     assert rc == -2  # group 20 > 16
