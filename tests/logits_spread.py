@@ -62,11 +62,12 @@ def _decode(dtype):
     return seam
 
 
-def oracle_runner(cfg: ModelConfig, model, attention_dtype=None) -> ModelRunner:
+def oracle_runner(cfg: ModelConfig, model, attention_dtype=None,
+                  block_size: int = 16) -> ModelRunner:
     """A CPU runner whose attention seams are the oracle: RoPE as the reference's torch ops,
     then write_kv + per-sequence SDPA (prefill) or the decode append + _decode_pytorch, in
     the model dtype (attention_dtype None) or computed in attention_dtype."""
-    r = ModelRunner(cfg, device="cpu", model=model)
+    r = ModelRunner(cfg, block_size, device="cpu", model=model)
     for layer in r.model.model.layers:
         att = layer.self_attn
         att.fuse_rope = False

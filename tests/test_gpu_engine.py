@@ -81,19 +81,24 @@ def drive(cfg, gpu, cpu, sched, max_steps=60):
     return agree, total, worst, steps, mixed
 
 
-def _twin_runners(cfg, seed, nb):
-    gpu = ModelRunner(cfg, device=DEV, model=random_init_(build_model(cfg), seed))
-    cpu = oracle_runner(cfg, random_init_(build_model(cfg), seed))
+def _twin_runners(cfg, seed, nb, block_size=16):
+    gpu = ModelRunner(cfg, block_size, device=DEV, model=random_init_(build_model(cfg), seed))
+    cpu = oracle_runner(cfg, random_init_(build_model(cfg), seed), block_size=block_size)
     gpu.init_kv_cache(nb)
     cpu.init_kv_cache(nb)
     return gpu, cpu
 
 
+@pytest.mark.parametrize("bs", [16, 64])
 @torch.no_grad()
-def test_toy_model_logits_match_reference_path():
+def test_toy_model_logits_match_reference_path(bs):
+    """Mixed prefill + decode steps through the scheduler against the CPU model with the
+    oracle seams, at the default page size and at 64-token pages (the reference's
+    --page-size: BlockAllocator, runner pools and tables all in blocks of that size)."""
     cfg = ModelConfig(**TOY)
-    gpu, cpu = _twin_runners(cfg, 3, 64)
-    sched = Scheduler(BlockAllocator(64, 0, 16), max_num_seqs=8, max_num_batched_tokens=600)
+    nb = 64 * 16 // bs
+    gpu, cpu = _twin_runners(cfg, 3, nb, bs)
+    sched = Scheduler(BlockAllocator(nb, 0, bs), max_num_seqs=8, max_num_batched_tokens=600)
     rng = np.random.default_rng(0)
     for i, n in enumerate([5, 31, 16, 70, 1, 120]):
         sched.add(SeqState(i + 1, f"r{i}", rng.integers(0, cfg.vocab_size, n).tolist(),
@@ -241,11 +246,12 @@ def test_qwen2_05b_teacher_forced_logits():
     assert agree >= 0.8 * total
 
 
+@pytest.mark.parametrize("bs", [16, 32])
 @torch.no_grad()
-def test_engine_runs_requests_to_completion():
+def test_engine_runs_requests_to_completion(bs):
     cfg = ModelConfig(**TOY)
-    eng = LLMEngine(cfg, max_gpu_blocks=256, seed=1, decode_graphs=True, max_model_len=512,
-                    max_num_seqs=16)
+    eng = LLMEngine(cfg, block_size=bs, max_gpu_blocks=256, seed=1, decode_graphs=True,
+                    max_model_len=512, max_num_seqs=16)
     rng = np.random.default_rng(1)
     want = {}
     for i in range(12):
