@@ -220,11 +220,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
   const int k_row = lane / CPR, k_chunk = lane % CPR;
   const int k_off = k_row * D + 8 * k_chunk;  // + RPI * D * s
   const int v_off = 4 * j * D + DPL * c;      // token rows 4j..4j+3, head_dim DPL*c..
-  // Per wave: a 16 x D K tile; with NW > 1 the same memory later holds each wave's
-  // accumulators ([E][64] floats, twice the tile) for the combine, then (m, l).
+  // Per wave: a 16 x D K tile.  With NW > 1 each wave's K tile sits at the start of a slot
+  // of [E][64] floats (twice the tile) that later holds the wave's accumulators for the
+  // combine, so that no wave writes LDS another wave may still be reading; (m, l) follow the
+  // slots.
   constexpr int kSmemFloats = NW == 1 ? 8 * D : NW * 64 * E + NW * 32;
   __shared__ __attribute__((aligned(16))) float smem[kSmemFloats];
-  u16* const ktile = reinterpret_cast<u16*>(smem) + wv * 16 * D;
+  u16* const ktile = NW == 1 ? reinterpret_cast<u16*>(smem) + wv * 16 * D
+                             : reinterpret_cast<u16*>(smem + wv * 64 * E);
   // Chunk q of row r lives at r*D + 8*(q ^ swz(r)): conflict-free for both the
   // row-layout writes and the A-operand reads.
   auto swz = [](int r) { return D == 128 ? (r & 15) : ((r >> 1) & 7); };
@@ -603,40 +606,45 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         a.block_table[(int64_t)seq * a.bt_row_stride + (col < a.max_blocks ? col : a.max_blocks - 1)];
     const int nt = seq_tiles(a, seq);
     if (wv < nt) segment(seq, wv, nt, nt, 0, &first_bt);
-    // Combine: every wave's m to LDS; each lane takes the maximum M over the waves for its
-    // head and scales its wave's accumulators and l by 2^(m - M) (one exponential per lane)
-    // into LDS (over the K tiles, dead once every wave is past the first barrier); then wave
-    // w sums elements w*KPW .. + KPW of every lane over the NW waves in a fixed order.  A
-    // sequence with nothing to attend (no tiles) comes out as zeros (attention.py:307-308 on
-    // an empty context).
-    static_assert(NW * 16 * D * 2 <= NW * 64 * E * 4, "m is stored past the K tiles");
+    // Combine: every wave writes its m, l and unscaled accumulators into its own LDS slot
+    // (over its own K tile: one wave's LDS accesses complete in order), one barrier; then
+    // each lane takes the maximum M over the waves for its head, and wave w sums elements
+    // w*KPW .. + KPW of every lane over the NW waves in a fixed order, each term scaled by
+    // 2^(m - M) (products rounded before the sum).  A sequence with nothing to attend (no
+    // tiles) comes out as zeros (attention.py:307-308 on an empty context).
+    static_assert(16 * D * 2 <= 64 * E * 4, "a wave's K tile fits its accumulator slot");
     constexpr int KPW = E / NW;
     static_assert(KPW * NW == E, "waves must divide the accumulator elements");
-    float* const sacc = smem;                 // [wave][E][64]: scaled accumulators
+    float* const sacc = smem;                 // [wave][E][64]: accumulators
     float* const sm = smem + NW * 64 * E;     // [wave][16]: m
-    float* const sl = sm + NW * 16;           // [wave][16]: scaled l
-    if (j == 0) sm[wv * 16 + c] = held_m;
-    __syncthreads();
-    float mx = kNegInf;
-#pragma unroll
-    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, sm[w * 16 + c]);
-    const float wt = held_m == kNegInf ? 0.f : fast_exp2(held_m - mx);
+    float* const sl = sm + NW * 16;           // [wave][16]: l
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
 #pragma unroll
-      for (int b = 0; b < DPL; ++b) sacc[(wv * E + DPL * i + b) * 64 + lane] = held[b][i] * wt;
+      for (int b = 0; b < DPL; ++b) sacc[(wv * E + DPL * i + b) * 64 + lane] = held[b][i];
     }
-    if (j == 0) sl[wv * 16 + c] = held_l * wt;
+    if (j == 0) {
+      sm[wv * 16 + c] = held_m;
+      sl[wv * 16 + c] = held_l;
+    }
     __syncthreads();
     if (!head_ok) return;
+    float mw[NW];
+    float mx = kNegInf;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) {
+      mw[w] = sm[w * 16 + c];
+      mx = fmaxf(mx, mw[w]);
+    }
     float den = 0.f, o[KPW];
 #pragma unroll
     for (int k = 0; k < KPW; ++k) o[k] = 0.f;
 #pragma unroll
     for (int w = 0; w < NW; ++w) {
-      den += sl[w * 16 + c];
+      const float wt = mw[w] == kNegInf ? 0.f : fast_exp2(mw[w] - mx);
+      den += __fmul_rn(sl[w * 16 + c], wt);
 #pragma unroll
-      for (int k = 0; k < KPW; ++k) o[k] += sacc[(w * E + wv * KPW + k) * 64 + lane];
+      for (int k = 0; k < KPW; ++k) o[k] += __fmul_rn(sacc[(w * E + wv * KPW + k) * 64 + lane], wt);
     }
     const float inv = den > 0.f ? 1.f / den : 0.f;
     u16* const out_row =
