@@ -52,7 +52,7 @@ extern "C" {
 /* Same object as hipStream_t; declared here so callers need no HIP headers. */
 typedef struct ihipStream_t* ndl_stream_t;
 
-#define NDL_ABI_VERSION 5
+#define NDL_ABI_VERSION 6
 
 enum ndl_status {
   NDL_OK = 0,
@@ -68,10 +68,13 @@ enum ndl_status {
 #define NDL_DECODE_STATIC_SCRATCH_BYTES (16u << 20)
 
 /* Element format of the pools and activations: the model dtypes the reference runs its
- * attention in (needle/args.py:80-84; float32 is not built).  Every entry point takes both. */
+ * attention in (needle/args.py:80-84, resolved at :143-153).  Every entry point takes all
+ * three; bf16 and fp16 run the MFMA kernels of the 16-bit formats, float32 its own kernels
+ * (fp32 MFMA, fp32 probabilities) with the same split, masking and combine rules. */
 enum ndl_dtype {
   NDL_DTYPE_BF16 = 0,
-  NDL_DTYPE_F16 = 1
+  NDL_DTYPE_F16 = 1,
+  NDL_DTYPE_F32 = 2
 };
 
 /* ABI version of the loaded library (NDL_ABI_VERSION at build time). */
@@ -97,7 +100,8 @@ const char* ndl_strerror(int status);
  *
  * k, v: [num_tokens][num_kv_heads][head_dim], token stride k_tok_stride /
  * v_tok_stride elements, rows inside a token contiguous.  The copy is
- * bit-exact.  Any head_dim that is a multiple of 8 is accepted.
+ * bit-exact.  Any head_dim whose rows are whole 16-byte chunks is accepted (a multiple of 8
+ * for bf16 and fp16, of 4 for float32).
  */
 int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int block_size,
                   int head_dim, int dtype,
@@ -116,13 +120,13 @@ int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int bloc
  * For every token t and every element d < head_dim, with half = head_dim / 2,
  *   rot(x)[d] = -x[d + half] (d < half), x[d - half] (d >= half)
  *   y[d]      = r( r(x[d] * cos[t][d]) + r(rot(x)[d] * sin[t][d]) )
- * with r the rounding to the element format (bf16 or fp16, nearest even), which is the
+ * with r the rounding to the element format (bf16, fp16 or fp32, nearest even), which is the
  * reference's op-by-op rounding in the model dtype (bit-exact).  q rotated is
  * written to q_out [num_tokens][num_heads][head_dim] (contiguous); k rotated and
  * v unchanged go to the cache slot that ndl_kv_append would pick for token t
  * (same slot rule, same handling of out-of-range block ids).  cos/sin:
  * [num_tokens][head_dim] with token stride cs_tok_stride.  head_dim must be a
- * multiple of 16.  q and q_out may both be NULL: then only k is rotated and
+ * multiple of 16 (8 for float32).  q and q_out may both be NULL: then only k is rotated and
  * k, v appended (for ndl_rope_varlen_prefill, which rotates q itself).
  */
 int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stride,
@@ -161,9 +165,11 @@ size_t ndl_paged_decode_workspace_bytes(int num_seqs, int num_heads, int num_kv_
  *   out[i][h][:] = softmax(scale * q[i][h] . K_i^T) V_i            (:307-308)
  * q: [num_seqs][num_heads][head_dim], token stride q_tok_stride.
  * out: [num_seqs][num_heads][head_dim] contiguous.  fp32 accumulation.
- * L_i <= 0 gives zeros.  Supported: bf16 and fp16, block_size 16, head_dim 64 or 128,
- * num_heads / num_kv_heads in 1..16.  The workspace (ndl_paged_decode_workspace_bytes)
- * is always required; calls that share one must not overlap.
+ * L_i <= 0 gives zeros.  Supported: bf16, fp16 and float32, block_size 16 to 1024 (powers
+ * of two), head_dim 64 or 128, num_heads / num_kv_heads in 1..16.  The workspace
+ * (ndl_paged_decode_workspace_bytes) is required for bf16 and fp16; calls that share one
+ * must not overlap.  float32 runs one workgroup per (kv head, sequence) whatever
+ * partition_tokens asks for (the value is still checked) and uses no workspace.
  */
 int ndl_paged_decode(void* out, const void* q, int64_t q_tok_stride,
                      const void* kv_cache, int64_t num_blocks,
@@ -320,7 +326,7 @@ int ndl_rope_varlen_prefill(void* out, const void* q, int64_t q_tok_stride,
  * (NDL_ERR_INVALID_ARG) before any launch.  src_ids / dst_ids: int32 [num_pairs] in device
  * memory or pinned host memory.  A pair with an id outside its pool is skipped.  Pairs
  * must not write one destination block twice.  One launch for all layers;
- * num_layers <= 128.  bf16 or fp16 (the copy is bit-exact either way).
+ * num_layers <= 128.  bf16, fp16 or float32 (the copy is bit-exact in every format).
  */
 int ndl_kv_block_copy(void* const* dst_pools, int64_t dst_num_blocks,
                       const void* const* src_pools, int64_t src_num_blocks,

@@ -15,10 +15,11 @@ import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 _PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = _PKG_DIR / "libneedle_amd.so"
 
-NDL_ABI_VERSION = 5
+NDL_ABI_VERSION = 6
 NDL_DECODE_STATIC_SCRATCH_BYTES = 16 << 20
 NDL_DTYPE_BF16 = 0
 NDL_DTYPE_F16 = 1
+NDL_DTYPE_F32 = 2
 
 # Every extern "C" symbol include/needle_amd.h declares.
 EXPORTED_SYMBOLS = (

@@ -46,9 +46,10 @@ constexpr int kAppendSmallSeqs = 63;
 // ROPE: k is rotated on the way (the rotary embedding of ndl_rope_kv_append, rope8, from
 // the token's cos/sin rows).  A lane then moves a chunk pair (c, c + head_dim/16) of one
 // row, the rotation's operands: items are the k rows' pairs, then the v rows' pairs (copied
-// unrotated), the same count as the chunks of one plane without ROPE.  F16: the rotation's
-// element format is fp16 (else bf16); the plain copy is format-free.
-template <int TPW, bool SMALL, bool ROPE, bool F16 = false>
+// unrotated), the same count as the chunks of one plane without ROPE.  FMT: the rotation's
+// element format (Fmt); the plain copy is format-free.  Sizes and offsets count 16-bit
+// units (a float32 row of D elements is 2D units; the launcher converts).
+template <int TPW, bool SMALL, bool ROPE, int FMT = kFmtBF16>
 __global__ __launch_bounds__(256) void kv_append_kernel(
     u16* __restrict__ cache, int64_t plane_elems, int64_t num_blocks, int num_kv_heads,
     int block_size, int head_dim,
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 #pragma unroll
     for (int u = 0; u < TPW; ++u) {
       u32x4 ol = xl[u], oh = xh[u];
-      if (!is_v) rope8<F16>(xl[u], xh[u], cl[u], ch[u], sl[u], sh[u], ol, oh);
+      if (!is_v) rope16<FMT>(xl[u], xh[u], cl[u], ch[u], sl[u], sh[u], ol, oh);
       if (live && dst_row[u] >= 0) {
         st16(plane + dst_row[u] + out_off, ol);
         st16(plane + dst_row[u] + out_off + half * 8, oh);
@@ -185,15 +186,21 @@ __global__ __launch_bounds__(256) void kv_append_kernel(
 }
 
 // Shared by ndl_kv_append and the k-only form of ndl_rope_kv_append (rope_cos != nullptr:
-// k rotated in the format of rope_f16; head_dim a multiple of 16).  Arguments are checked by
-// the callers.
+// k rotated in format fmt; head_dim a multiple of 16).  head_dim and the strides count
+// elements of format fmt.  Arguments are checked by the callers.
 int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int block_size,
                      int head_dim, const void* k, int64_t k_tok_stride, const void* v,
                      int64_t v_tok_stride, const int32_t* block_table, int64_t bt_row_stride,
                      int max_blocks_per_seq, const int32_t* cu_seqlens,
                      const int32_t* context_lens, int num_seqs, int64_t num_tokens,
                      const void* rope_cos, const void* rope_sin, int64_t rope_stride,
-                     bool rope_f16, ndl_stream_t stream) {
+                     int fmt, ndl_stream_t stream) {
+  if (fmt == kFmtF32) {   // the kernel counts 16-bit units
+    head_dim *= 2;
+    k_tok_stride *= 2;
+    v_tok_stride *= 2;
+    rope_stride *= 2;
+  }
   const int64_t plane_elems = num_blocks * num_kv_heads * (int64_t)block_size * head_dim;
   const bool small = cu_seqlens != nullptr && num_seqs <= kAppendSmallSeqs;
   const bool rope = rope_cos != nullptr;
@@ -211,11 +218,12 @@ int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int b
 #define NDL_APPEND_FNS(S, R, F)                                                           \
   {(const void*)kv_append_kernel<1, S, R, F>, (const void*)kv_append_kernel<2, S, R, F>,  \
    (const void*)kv_append_kernel<3, S, R, F>, (const void*)kv_append_kernel<4, S, R, F>}
-  // [copy, rotate bf16, rotate fp16][small][tokens per wave - 1]
-  const void* fns[3][2][kAppendMaxTokensPerWave] = {
-      {NDL_APPEND_FNS(false, false, false), NDL_APPEND_FNS(true, false, false)},
-      {NDL_APPEND_FNS(false, true, false), NDL_APPEND_FNS(true, true, false)},
-      {NDL_APPEND_FNS(false, true, true), NDL_APPEND_FNS(true, true, true)}};
+  // [copy, rotate bf16, rotate fp16, rotate fp32][small][tokens per wave - 1]
+  const void* fns[4][2][kAppendMaxTokensPerWave] = {
+      {NDL_APPEND_FNS(false, false, kFmtBF16), NDL_APPEND_FNS(true, false, kFmtBF16)},
+      {NDL_APPEND_FNS(false, true, kFmtBF16), NDL_APPEND_FNS(true, true, kFmtBF16)},
+      {NDL_APPEND_FNS(false, true, kFmtF16), NDL_APPEND_FNS(true, true, kFmtF16)},
+      {NDL_APPEND_FNS(false, true, kFmtF32), NDL_APPEND_FNS(true, true, kFmtF32)}};
 #undef NDL_APPEND_FNS
   u16* cache = (u16*)kv_cache;
   const u16* kp = (const u16*)k;
@@ -226,7 +234,7 @@ int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int b
                   &head_dim, &kp, &k_tok_stride, &vp, &v_tok_stride, &block_table,
                   &bt_row_stride, &max_blocks_per_seq, &cu_seqlens, &context_lens, &num_seqs,
                   &num_tokens, &cp, &sp, &rope_stride};
-  if (hipLaunchKernel(fns[rope ? (rope_f16 ? 2 : 1) : 0][small ? 1 : 0][tpw - 1],
+  if (hipLaunchKernel(fns[rope ? 1 + fmt : 0][small ? 1 : 0][tpw - 1],
                       dim3((unsigned)blocks),
                       dim3(256), args, 0, (hipStream_t)stream) != hipSuccess) {
     (void)hipGetLastError();  // clear the error so that the next call's check sees its own
@@ -246,8 +254,10 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
                              const int32_t* cu_seqlens, const int32_t* context_lens,
                              int num_seqs, int64_t num_tokens, ndl_stream_t stream) {
   using namespace ndl;
-  if (dtype != NDL_DTYPE_BF16 && dtype != NDL_DTYPE_F16) return NDL_ERR_UNSUPPORTED;
-  if (head_dim <= 0 || head_dim % 8 != 0 || block_size <= 0) return NDL_ERR_UNSUPPORTED;
+  if (!dtype_known(dtype)) return NDL_ERR_UNSUPPORTED;
+  // 16-byte rows: a multiple of 8 16-bit elements or of 4 float32 ones
+  if (head_dim <= 0 || head_dim % (dtype_is_f32(dtype) ? 4 : 8) != 0 || block_size <= 0)
+    return NDL_ERR_UNSUPPORTED;
   if (num_tokens < 0 || num_seqs < 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
       max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq)
     return NDL_ERR_INVALID_ARG;
@@ -260,10 +270,11 @@ extern "C" int ndl_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_head
     return NDL_ERR_INVALID_ARG;
   // 16-byte vector access needs 16-byte aligned rows.
   if (((uintptr_t)kv_cache | (uintptr_t)k | (uintptr_t)v) & 15u) return NDL_ERR_INVALID_ARG;
-  if ((k_tok_stride | v_tok_stride) & 7) return NDL_ERR_INVALID_ARG;
+  if ((k_tok_stride | v_tok_stride) & (dtype_is_f32(dtype) ? 3 : 7)) return NDL_ERR_INVALID_ARG;
 
   return launch_kv_append(kv_cache, num_blocks, num_kv_heads, block_size, head_dim, k,
                           k_tok_stride, v, v_tok_stride, block_table, bt_row_stride,
                           max_blocks_per_seq, cu_seqlens, context_lens, num_seqs, num_tokens,
-                          nullptr, nullptr, 0, false, stream);
+                          nullptr, nullptr, 0, dtype_is_f32(dtype) ? kFmtF32 : kFmtBF16,
+                          stream);
 }

@@ -72,14 +72,14 @@ extern "C" int ndl_kv_block_copy(void* const* dst_pools, int64_t dst_num_blocks,
                                  int dtype, const int32_t* src_ids, const int32_t* dst_ids,
                                  int num_pairs, ndl_stream_t stream) {
   using namespace ndl;
-  if (dtype != NDL_DTYPE_BF16 && dtype != NDL_DTYPE_F16) return NDL_ERR_UNSUPPORTED;
+  if (!dtype_known(dtype)) return NDL_ERR_UNSUPPORTED;
   if (num_layers < 0 || num_pairs < 0 || num_kv_heads <= 0 || block_size <= 0 ||
       head_dim <= 0 || dst_num_blocks <= 0 || src_num_blocks <= 0)
     return NDL_ERR_INVALID_ARG;
   if (num_layers > kSwapMaxLayers) return NDL_ERR_UNSUPPORTED;
   if (num_layers == 0 || num_pairs == 0) return NDL_OK;
   if (!dst_pools || !src_pools || !src_ids || !dst_ids) return NDL_ERR_INVALID_ARG;
-  const int64_t row_bytes = (int64_t)num_kv_heads * block_size * head_dim * 2;
+  const int64_t row_bytes = (int64_t)num_kv_heads * block_size * head_dim * dtype_bytes(dtype);
   if (row_bytes % 16) return NDL_ERR_UNSUPPORTED;
   SwapArgs a;
   for (int l = 0; l < num_layers; ++l) {

@@ -132,6 +132,36 @@ __device__ __forceinline__ void rope8(const u32x4& lo, const u32x4& hi, const u3
   }
 }
 
+// The same rotation in float32 (the reference's --dtype float32): 4 elements of each half
+// per 16 bytes, every product and the sum rounded to fp32 (contraction off: the reference's
+// x * cos + rotate_half(x) * sin is two multiplies and an add).
+__device__ __forceinline__ void rope4_f32(const u32x4& lo, const u32x4& hi, const u32x4& clo,
+                                          const u32x4& chi, const u32x4& slo, const u32x4& shi,
+                                          u32x4& out_lo, u32x4& out_hi) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const float xl = __uint_as_float(lo[w]), xh = __uint_as_float(hi[w]);
+    const float nxh = __uint_as_float(hi[w] ^ 0x80000000u);   // -x_hi, exact
+    out_lo[w] = __float_as_uint(xl * __uint_as_float(clo[w]) + nxh * __uint_as_float(slo[w]));
+    out_hi[w] = __float_as_uint(xh * __uint_as_float(chi[w]) + xl * __uint_as_float(shi[w]));
+  }
+}
+
+// Element formats on the device: the ABI dtype codes (NDL_DTYPE_*).
+enum Fmt { kFmtBF16 = 0, kFmtF16 = 1, kFmtF32 = 2 };
+
+// The rotation of 16 bytes of each half in format FMT (8 16-bit or 4 fp32 elements).
+template <int FMT>
+__device__ __forceinline__ void rope16(const u32x4& lo, const u32x4& hi, const u32x4& clo,
+                                       const u32x4& chi, const u32x4& slo, const u32x4& shi,
+                                       u32x4& out_lo, u32x4& out_hi) {
+  if constexpr (FMT == kFmtF32)
+    rope4_f32(lo, hi, clo, chi, slo, shi, out_lo, out_hi);
+  else
+    rope8<FMT == kFmtF16>(lo, hi, clo, chi, slo, shi, out_lo, out_hi);
+}
+
 // Block sizes the attention kernels take: powers of two from 16 to 1024 tokens, each block
 // read as 16-token tiles.  log2(block_size / 16), or -1 for any other size.
 constexpr int kMaxBlockSize = 1024;
@@ -145,9 +175,15 @@ inline int block_tile_shift(int block_size) {
 
 // The element format of an ABI dtype code (false: bf16, true: fp16); false for others.
 inline bool dtype_is_f16(int dtype) { return dtype == NDL_DTYPE_F16; }
+inline bool dtype_is_f32(int dtype) { return dtype == NDL_DTYPE_F32; }
+// The 16-bit formats (the MFMA kernels' element formats).
 inline bool dtype_supported(int dtype) {
   return dtype == NDL_DTYPE_BF16 || dtype == NDL_DTYPE_F16;
 }
+// Any format the library takes.
+inline bool dtype_known(int dtype) { return dtype_supported(dtype) || dtype == NDL_DTYPE_F32; }
+// Bytes per element.
+inline int dtype_bytes(int dtype) { return dtype == NDL_DTYPE_F32 ? 4 : 2; }
 
 // exp2 on the hardware transcendental unit (v_exp_f32).
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -225,14 +261,33 @@ inline int64_t resident_workgroups(const void* fn, int block) {
   return wgs;
 }
 
-// The append launcher of kv_append.hip (rope_cos != nullptr: k rotated by rope8 in the
-// format rope_f16 names).
+// The append launcher of kv_append.hip (rope_cos != nullptr: k rotated in format fmt, a
+// Fmt; head_dim and strides in elements of that format).
 int launch_kv_append(void* kv_cache, int64_t num_blocks, int num_kv_heads, int block_size,
                      int head_dim, const void* k, int64_t k_tok_stride, const void* v,
                      int64_t v_tok_stride, const int32_t* block_table, int64_t bt_row_stride,
                      int max_blocks_per_seq, const int32_t* cu_seqlens,
                      const int32_t* context_lens, int num_seqs, int64_t num_tokens,
                      const void* rope_cos, const void* rope_sin, int64_t rope_stride,
-                     bool rope_f16, ndl_stream_t stream);
+                     int fmt, ndl_stream_t stream);
+
+// The float32 attention launchers (paged_decode_f32.hip, varlen_prefill_f32.hip); the entry
+// points check the arguments common to all formats first.  k_new/v_new non-null: the step's
+// rows are appended first (by ndl_kv_append's kernel); cos/sin non-null: q (and k_new) are
+// rotated.
+int launch_decode_f32(void* out, const void* q, int64_t q_tok_stride, const void* k_new,
+                      int64_t k_tok_stride, const void* v_new, int64_t v_tok_stride,
+                      const void* cos, const void* sin, int64_t cs_tok_stride, void* kv_cache,
+                      int64_t num_blocks, const int32_t* block_table, int64_t bt_row_stride,
+                      int max_blocks_per_seq, const int32_t* context_lens, int num_seqs,
+                      int num_heads, int num_kv_heads, int head_dim, int block_size, float scale,
+                      ndl_stream_t stream);
+int launch_prefill_f32(void* out, const void* q, int64_t q_tok_stride, const void* cos,
+                       const void* sin, int64_t cs_tok_stride, const void* kv_cache,
+                       int64_t num_blocks, const int32_t* block_table, int64_t bt_row_stride,
+                       int max_blocks_per_seq, const int32_t* cu_seqlens,
+                       const int32_t* context_lens, int num_seqs, int64_t num_tokens,
+                       int max_seqlen, int max_context_len, int num_heads, int num_kv_heads,
+                       int head_dim, int block_size, float scale, ndl_stream_t stream);
 
 }  // namespace ndl

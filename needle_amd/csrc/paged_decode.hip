@@ -1015,7 +1015,7 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
                          const void* v_new, int64_t v_new_stride, ndl_stream_t stream,
                          bool static_scratch = false, const void* rope_cos = nullptr,
                          const void* rope_sin = nullptr, int64_t rope_stride = 0) {
-  if (!dtype_supported(dtype)) return NDL_ERR_UNSUPPORTED;
+  if (!dtype_known(dtype)) return NDL_ERR_UNSUPPORTED;
   const int tshift = block_tile_shift(block_size);
   if (tshift < 0 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -1032,6 +1032,17 @@ static int launch_decode(void* out, const void* q, int64_t q_tok_stride, const v
   if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)kv_cache) & 15u) return NDL_ERR_INVALID_ARG;
   if (q_tok_stride & 7) return NDL_ERR_INVALID_ARG;
   if (num_seqs > 65535) return NDL_ERR_UNSUPPORTED;
+  if (dtype_is_f32(dtype)) {
+    // One workgroup per (kv head, sequence) whatever the split asks for (the values are
+    // checked as for the other formats); no partials, so neither workspace nor scratch.
+    if (partition_tokens < -1 || (partition_tokens > 0 && partition_tokens % 16 != 0))
+      return NDL_ERR_INVALID_ARG;
+    return launch_decode_f32(out, q, q_tok_stride, k_new, k_new_stride, v_new, v_new_stride,
+                             rope_cos, rope_sin, rope_stride, const_cast<void*>(kv_cache),
+                             num_blocks, block_table, bt_row_stride, max_blocks_per_seq,
+                             context_lens, num_seqs, num_heads, num_kv_heads, head_dim,
+                             block_size, scale, stream);
+  }
   DecodeLayout lay;
   const int64_t max_tiles = (int64_t)max_blocks_per_seq << tshift;
   if (max_tiles > 0x7fffffff) return NDL_ERR_UNSUPPORTED;

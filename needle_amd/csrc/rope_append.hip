@@ -6,12 +6,13 @@
 // scatter; here one launch rotates q (written to q_out), rotates k and copies v
 // straight into their cache slots.
 //
-// Rounding is the reference's, op for op, in the model dtype r (bf16 or fp16):
+// Rounding is the reference's, op for op, in the model dtype r (bf16, fp16 or fp32):
 //   out[d] = r( r(x[d] * cos[d]) + r(rot(x)[d] * sin[d]) )
 // with rot(x)[d] = -x[d + D/2] (d < D/2) or x[d - D/2] (d >= D/2); every
-// product and the sum are formed in fp32 from 16-bit operands and rounded to
-// nearest-even, exactly as torch does for bf16 and fp16 tensors.  The result is
-// bit-identical to the reference's.
+// product and the sum are formed in fp32 and rounded to the format, nearest even,
+// exactly as torch does for bf16, fp16 and fp32 tensors.  The result is bit-identical to
+// the reference's.  Sizes and offsets count 16-bit units (a float32 row of D elements is
+// 2D units, its 16-byte chunks 4 elements; the entry point converts).
 #include "ndl_common.hpp"
 
 namespace ndl {
@@ -83,7 +84,7 @@ __device__ __forceinline__ int64_t kv_slot_row(const RopeArgs& a, int64_t t) {
 // cache.  Lanes past the last item load a valid item again and store nothing, so no
 // divergent branch separates the loads.  (A lane chooses between two row bases at most:
 // a three-way choice of pointers compiles to a lookup table in scratch memory.)
-template <bool F16>
+template <int FMT>
 __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t w =
@@ -112,7 +113,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
     const u32x4 slo = ld16(sn + d0), shi = ld16(sn + d0 + half);
     const int64_t krow = kv_slot_row(a, t);
     u32x4 olo, ohi;
-    rope8<F16>(lo, hi, clo, chi, slo, shi, olo, ohi);
+    rope16<FMT>(lo, hi, clo, chi, slo, shi, olo, ohi);
     if (is_v) {
       olo = lo;
       ohi = hi;
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(256) void rope_kv_append_kernel(RopeArgs a) {
     const u32x4 clo = ld16(cs + d0), chi = ld16(cs + d0 + half);
     const u32x4 slo = ld16(sn + d0), shi = ld16(sn + d0 + half);
     u32x4 olo, ohi;
-    rope8<F16>(lo, hi, clo, chi, slo, shi, olo, ohi);
+    rope16<FMT>(lo, hi, clo, chi, slo, shi, olo, ohi);
     if (live) {
       u16* const dst = a.q_out + (t * H + row) * (int64_t)D;
       st16(dst + d0, olo);
@@ -153,8 +154,10 @@ extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stri
                                   const int32_t* context_lens, int num_seqs, int64_t num_tokens,
                                   ndl_stream_t stream) {
   using namespace ndl;
-  if (!dtype_supported(dtype)) return NDL_ERR_UNSUPPORTED;
-  if (head_dim <= 0 || head_dim % 16 != 0 || block_size <= 0) return NDL_ERR_UNSUPPORTED;
+  if (!dtype_known(dtype)) return NDL_ERR_UNSUPPORTED;
+  // halves of whole 16-byte chunks: a multiple of 16 16-bit elements or of 8 float32 ones
+  if (head_dim <= 0 || head_dim % (dtype_is_f32(dtype) ? 8 : 16) != 0 || block_size <= 0)
+    return NDL_ERR_UNSUPPORTED;
   if (num_tokens < 0 || num_seqs < 0 || num_heads <= 0 || num_kv_heads <= 0 || num_blocks <= 0 ||
       max_blocks_per_seq <= 0 || bt_row_stride < max_blocks_per_seq)
     return NDL_ERR_INVALID_ARG;
@@ -170,13 +173,23 @@ extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stri
   if (((uintptr_t)q_out | (uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)cos |
        (uintptr_t)sin | (uintptr_t)kv_cache) & 15u)
     return NDL_ERR_INVALID_ARG;
-  if ((q_tok_stride | k_tok_stride | v_tok_stride | cs_tok_stride) & 7) return NDL_ERR_INVALID_ARG;
+  if ((q_tok_stride | k_tok_stride | v_tok_stride | cs_tok_stride) &
+      (dtype_is_f32(dtype) ? 3 : 7))
+    return NDL_ERR_INVALID_ARG;
 
+  const int fmt = dtype_is_f32(dtype) ? kFmtF32 : dtype_is_f16(dtype) ? kFmtF16 : kFmtBF16;
   if (q == nullptr)  // k rotated and k, v appended: the append kernel with the rotation
     return launch_kv_append(kv_cache, num_blocks, num_kv_heads, block_size, head_dim, k,
                             k_tok_stride, v, v_tok_stride, block_table, bt_row_stride,
                             max_blocks_per_seq, cu_seqlens, context_lens, num_seqs, num_tokens,
-                            cos, sin, cs_tok_stride, dtype_is_f16(dtype), stream);
+                            cos, sin, cs_tok_stride, fmt, stream);
+  if (fmt == kFmtF32) {   // the kernel counts 16-bit units
+    head_dim *= 2;
+    q_tok_stride *= 2;
+    k_tok_stride *= 2;
+    v_tok_stride *= 2;
+    cs_tok_stride *= 2;
+  }
   RopeArgs a;
   a.q_out = (u16*)q_out;
   a.q = (const u16*)q;
@@ -207,11 +220,14 @@ extern "C" int ndl_rope_kv_append(void* q_out, const void* q, int64_t q_tok_stri
   const int64_t rounds = (2 * num_kv_heads * cph + 63) / 64 + (num_heads * cph + 63) / 64;
   const int64_t blocks = (num_tokens * rounds + 3) / 4;
   if (blocks > 0x7fffffff) return NDL_ERR_INVALID_ARG;
-  if (dtype_is_f16(dtype))
-    hipLaunchKernelGGL(rope_kv_append_kernel<true>, dim3((unsigned)blocks), dim3(256), 0,
+  if (fmt == kFmtF32)
+    hipLaunchKernelGGL(rope_kv_append_kernel<kFmtF32>, dim3((unsigned)blocks), dim3(256), 0,
+                       (hipStream_t)stream, a);
+  else if (fmt == kFmtF16)
+    hipLaunchKernelGGL(rope_kv_append_kernel<kFmtF16>, dim3((unsigned)blocks), dim3(256), 0,
                        (hipStream_t)stream, a);
   else
-    hipLaunchKernelGGL(rope_kv_append_kernel<false>, dim3((unsigned)blocks), dim3(256), 0,
+    hipLaunchKernelGGL(rope_kv_append_kernel<kFmtBF16>, dim3((unsigned)blocks), dim3(256), 0,
                        (hipStream_t)stream, a);
   return check_launch();
 }

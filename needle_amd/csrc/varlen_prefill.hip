@@ -1038,7 +1038,7 @@ static int launch_prefill(void* out, const void* q, int64_t q_tok_stride, const 
                           int max_seqlen, int max_context_len, int num_heads, int num_kv_heads,
                           int head_dim, int block_size, int dtype, float scale,
                           ndl_stream_t stream) {
-  if (!dtype_supported(dtype)) return NDL_ERR_UNSUPPORTED;
+  if (!dtype_known(dtype)) return NDL_ERR_UNSUPPORTED;
   const int tshift = block_tile_shift(block_size);
   if (tshift < 0 || (head_dim != 64 && head_dim != 128)) return NDL_ERR_UNSUPPORTED;
   if (num_kv_heads <= 0 || num_heads <= 0 || num_heads % num_kv_heads != 0)
@@ -1057,6 +1057,12 @@ static int launch_prefill(void* out, const void* q, int64_t q_tok_stride, const 
     return NDL_ERR_INVALID_ARG;
   if (((uintptr_t)out | (uintptr_t)q | (uintptr_t)kv_cache) & 15u) return NDL_ERR_INVALID_ARG;
   if (q_tok_stride & 7) return NDL_ERR_INVALID_ARG;
+  if (dtype_is_f32(dtype))
+    return launch_prefill_f32(out, q, q_tok_stride, cos, sin, cs_tok_stride, kv_cache,
+                              num_blocks, block_table, bt_row_stride, max_blocks_per_seq,
+                              cu_seqlens, context_lens, num_seqs, num_tokens, max_seqlen,
+                              max_context_len, num_heads, num_kv_heads, head_dim, block_size,
+                              scale, stream);
   (void)max_context_len;
 
   const int group = num_heads / num_kv_heads;

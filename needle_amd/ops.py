@@ -19,7 +19,8 @@ import torch
 
 from . import _lib
 
-_DTYPES = {torch.bfloat16: _lib.NDL_DTYPE_BF16, torch.float16: _lib.NDL_DTYPE_F16}
+_DTYPES = {torch.bfloat16: _lib.NDL_DTYPE_BF16, torch.float16: _lib.NDL_DTYPE_F16,
+           torch.float32: _lib.NDL_DTYPE_F32}
 
 
 def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
@@ -124,7 +125,7 @@ def rope_kv_append(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor,
 
     Same result as _apply_rope (attention.py:88, :277-288) followed by the append
     of attention.py:141-154 (cu_seqlens=None) or _write_kv (:204-246), bit for bit.
-    q [T, H, D], k/v [T, Hkv, D], cos/sin [T, D] in the cache dtype (bf16 or fp16).
+    q [T, H, D], k/v [T, Hkv, D], cos/sin [T, D] in the cache dtype (bf16, fp16 or fp32).
     q=None rotates and appends k (and appends v) only, and returns None: the form that
     precedes rope_varlen_prefill, which rotates q itself.
     """
@@ -393,7 +394,7 @@ def kv_block_copy(dst_pools, src_pools, src_ids: torch.Tensor, dst_ids: torch.Te
     def check_pool(t, nb):
         _require(t.dim() == 5 and tuple(t.shape[2:]) == tuple(ref.shape[2:]) and t.shape[0] == 2
                  and t.shape[1] == nb, f"pool shape {tuple(t.shape)} differs from its set")
-        _require(t.dtype == ref.dtype and t.dtype in _DTYPES, "pools must share a 16-bit dtype",
+        _require(t.dtype == ref.dtype and t.dtype in _DTYPES, "pools must share one supported dtype",
                  TypeError)
         _require(t.is_contiguous(), "pools must be contiguous")
         _require(t.device == dev or (t.device.type == "cpu" and t.is_pinned()),
