@@ -32,13 +32,15 @@
 // A second kernel merges the partials of the sequences that span waves and writes
 // zeros for sequences with nothing to attend.
 //
-// Small batches (kv heads x sequences x NW waves within the resident waves, at most 16
-// tiles per wave): one workgroup of NW waves (16 at head_dim 64, 8 at 128) per (kv head,
+// Small batches (kv heads x sequences x NW waves within the resident waves, at most 32
+// tiles per wave at head_dim 64, 16 at 128): one workgroup of NW = 8 waves per (kv head,
 // sequence) instead.  Wave w takes every NW-th tile (w, w + NW, ..) through the same
-// per-tile code, and the waves
-// combine their (m, l, acc) through LDS: one launch, no workspace traffic.  With few
-// sequences the stream split would cut every sequence into many 2-tile pieces and the
-// merge kernel would cost as much as the attention.
+// per-tile code, and the waves combine their (m, l, acc) through LDS with one barrier: one
+// launch, no workspace traffic.  With few sequences the stream split would cut every
+// sequence into many 2-tile pieces and the merge kernel would cost as much as the attention.
+//
+// float32 pools and activations go to paged_decode_f32.hip (the entry points below check the
+// arguments every format shares, then dispatch).
 #include <stdlib.h>
 
 #include "ndl_common.hpp"

@@ -246,12 +246,15 @@ def test_qwen2_05b_teacher_forced_logits():
     assert agree >= 0.8 * total
 
 
-@pytest.mark.parametrize("bs", [16, 32])
+@pytest.mark.parametrize("bs,dtype", [(16, "bfloat16"), (32, "bfloat16"), (16, "float16"),
+                                      (16, "float32")])
 @torch.no_grad()
-def test_engine_runs_requests_to_completion(bs):
+def test_engine_runs_requests_to_completion(bs, dtype):
+    """The engine with graph-replayed decode steps, at two block sizes and in each model dtype
+    the reference's --dtype offers (needle/args.py:80-84)."""
     cfg = ModelConfig(**TOY)
     eng = LLMEngine(cfg, block_size=bs, max_gpu_blocks=256, seed=1, decode_graphs=True,
-                    max_model_len=512, max_num_seqs=16)
+                    max_model_len=512, max_num_seqs=16, dtype=dtype)
     rng = np.random.default_rng(1)
     want = {}
     for i in range(12):
