@@ -3,7 +3,8 @@
 Same constructor, the same forward() signature and meaning
 (attention.py:36-96), the same parameter names (q_proj/k_proj/v_proj/o_proj),
 and the same KV pool layout [2, num_blocks, num_kv_heads, block_size,
-head_dim].  Projections stay torch GEMMs (attention.py:84-86).  The rest of
+head_dim].  Projections stay torch GEMMs (attention.py:84-86); fuse_projections()
+runs the three as one GEMM over their concatenated weights.  The rest of
 forward is, bit-exact with the reference's bf16 rounding of RoPE (attention.py:88,
 277-288):
 
@@ -35,9 +36,55 @@ import math
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 from .. import ops
 from ..model.config import ModelConfig
+
+
+def fuse_linears(*mods: nn.Linear):
+    """Puts the weights (and biases) of Linear layers that read the same input into one
+    tensor, each layer's parameters becoming views of it, so that one GEMM serves them all
+    (F.linear over the fused weight, its output split).  Parameter names, values and
+    sharing with in-place updates are unchanged; the fused (weight, bias or None) is returned.
+    Moving the layers afterwards gives them separate storage again, which fused_outputs
+    detects."""
+    rows = [m.weight.shape[0] for m in mods]
+    w = torch.cat([m.weight.detach() for m in mods], 0)
+    b = None
+    if mods[0].bias is not None:
+        b = torch.cat([m.bias.detach() for m in mods], 0)
+    r0 = 0
+    for m, r in zip(mods, rows):
+        m.weight = nn.Parameter(w[r0:r0 + r], requires_grad=m.weight.requires_grad)
+        if b is not None:
+            m.bias = nn.Parameter(b[r0:r0 + r], requires_grad=m.bias.requires_grad)
+        r0 += r
+    return (w, b)
+
+
+def _still_fused(fused, mods) -> bool:
+    """True while every layer's weight (and bias) is the view fuse_linears made of the fused
+    tensor (a later .to() or a replaced parameter gives it storage of its own)."""
+    w, b = fused
+    r0 = 0
+    for m in mods:
+        r = m.weight.shape[0]
+        if m.weight.data_ptr() != w[r0:r0 + r].data_ptr() or m.weight.device != w.device:
+            return False
+        if b is not None and (m.bias is None or m.bias.data_ptr() != b[r0:r0 + r].data_ptr()):
+            return False
+        r0 += r
+    return r0 == w.shape[0]
+
+
+def fused_outputs(fused, mods, x):
+    """The outputs of the Linear layers mods on x: one GEMM over the fused weight while their
+    parameters are still views of it (fuse_linears), otherwise one per layer."""
+    if fused is not None and _still_fused(fused, mods):
+        w, b = fused
+        return F.linear(x, w, b).split([m.weight.shape[0] for m in mods], dim=-1)
+    return tuple(m(x) for m in mods)
 
 
 def apply_rope(q, k, cos, sin):
@@ -75,15 +122,23 @@ class Attention(nn.Module):
         # HIP graph captured with an older one keeps writing it on every replay.
         self._workspaces = []
         self.fuse_rope = True
+        self._qkv = None   # fused q/k/v projection (fuse_projections)
+
+    def fuse_projections(self) -> None:
+        """One GEMM for the q, k and v projections (they read the same input), their
+        parameters becoming views of one tensor; call after the weights are in place."""
+        self._qkv = fuse_linears(self.q_proj, self.k_proj, self.v_proj)
 
     def forward(self, hidden_states: torch.Tensor, positions: torch.Tensor,
                 kv_cache: torch.Tensor, block_table: torch.Tensor, cu_seqlens: torch.Tensor,
                 context_lens: torch.Tensor, max_seqlen: int, is_prefill: bool,
                 cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
         total = hidden_states.shape[0]
-        q = self.q_proj(hidden_states).view(total, self.num_heads, self.head_dim)
-        k = self.k_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
-        v = self.v_proj(hidden_states).view(total, self.num_kv_heads, self.head_dim)
+        q, k, v = fused_outputs(self._qkv, (self.q_proj, self.k_proj, self.v_proj),
+                                hidden_states)
+        q = q.view(total, self.num_heads, self.head_dim)
+        k = k.view(total, self.num_kv_heads, self.head_dim)
+        v = v.view(total, self.num_kv_heads, self.head_dim)
         if self.fuse_rope:
             if is_prefill:
                 ops.rope_kv_append(None, k, v, cos, sin, kv_cache, block_table, context_lens,

@@ -1,8 +1,21 @@
-"""RMSNorm (reference needle/layers/norm.py:8-17): x * rsqrt(mean(x^2) + eps) in fp32, times weight."""
+"""RMSNorm (reference needle/layers/norm.py:8-17).
+
+The reference computes, in torch ops,
+    y = (x * rsqrt(mean(x.float()^2) + eps)).to(dtype)     fp32 statistic and product
+    out = weight * y                                      rounded in the model dtype
+which is five elementwise kernels and a reduction before the weight product.  Here the
+first line is torch's fused RMS normalisation without a weight (the same fp32 statistic and
+product, one rounding to x's dtype, in one kernel) and the weight product stays its own op,
+so the output keeps the reference's two roundings.  Against the reference's op sequence
+(tests/test_norm.py): the same bits on the CPU; on the GPU the fused statistic and
+reciprocal square root can differ in their last bit, which moves an element by an ulp of
+the format now and then.
+"""
 from __future__ import annotations
 
 import torch
 import torch.nn as nn
+import torch.nn.functional as F
 
 
 class RMSNorm(nn.Module):
@@ -12,6 +25,5 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(hidden_size))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        variance = x.float().pow(2).mean(-1, keepdim=True)
-        x = x * torch.rsqrt(variance + self.eps)
-        return self.weight * x.to(self.weight.dtype)
+        y = F.rms_norm(x, (x.shape[-1],), None, self.eps)
+        return self.weight * y.to(self.weight.dtype)

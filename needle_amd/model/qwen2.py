@@ -15,7 +15,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
-from ..layers.attention import Attention
+from ..layers.attention import Attention, fuse_linears, fused_outputs
 from ..layers.norm import RMSNorm
 from ..layers.rope import RotaryEmbedding
 from .config import ModelConfig
@@ -27,9 +27,15 @@ class MLP(nn.Module):
         self.gate_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.up_proj = nn.Linear(config.hidden_size, config.intermediate_size, bias=False)
         self.down_proj = nn.Linear(config.intermediate_size, config.hidden_size, bias=False)
+        self._gate_up = None   # fused gate/up projection (fuse_projections)
+
+    def fuse_projections(self) -> None:
+        """One GEMM for the gate and up projections (they read the same input)."""
+        self._gate_up = fuse_linears(self.gate_proj, self.up_proj)
 
     def forward(self, x):
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+        gate, up = fused_outputs(self._gate_up, (self.gate_proj, self.up_proj), x)
+        return self.down_proj(F.silu(gate) * up)
 
 
 class DecoderLayer(nn.Module):
@@ -87,6 +93,16 @@ class CausalLM(nn.Module):
                        max_seqlen, is_prefill)
         last = h[cu_seqlens[1:].long() - 1] if is_prefill else h
         return self.lm_head(last)
+
+
+def fuse_projections(model: nn.Module) -> nn.Module:
+    """Runs every layer's q/k/v and gate/up projections as one GEMM each (the weights
+    concatenated, the parameters views of them); call once the weights are in place and the
+    model is on its device."""
+    for m in model.modules():
+        if m is not model and hasattr(m, "fuse_projections"):
+            m.fuse_projections()
+    return model
 
 
 def build_model(config: ModelConfig) -> CausalLM:

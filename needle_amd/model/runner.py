@@ -32,7 +32,7 @@ from .. import ops
 from ..backend.request import SeqState
 from ..backend.scheduler import StepPlan
 from .config import ModelConfig
-from .qwen2 import build_model, random_init_
+from .qwen2 import build_model, fuse_projections, random_init_
 from .sampler import check_greedy, sample
 
 
@@ -182,7 +182,8 @@ class ModelRunner:
     DEFAULT_BUCKETS = (1, 2, 4, 8, 12, 16, 24, 32, 48, 64, 96, 128, 192, 256)
 
     def __init__(self, model_config: ModelConfig, block_size: int = 16, dtype: str = "bfloat16",
-                 device: str = "cuda:0", seed: int = 0, model: Optional[torch.nn.Module] = None):
+                 device: str = "cuda:0", seed: int = 0, model: Optional[torch.nn.Module] = None,
+                 fuse: bool = True):
         self.model_config = model_config
         self.block_size = block_size
         self.device = torch.device(device)
@@ -190,6 +191,8 @@ class ModelRunner:
         if model is None:
             model = random_init_(build_model(model_config), seed)
         self.model = model.to(device=self.device, dtype=self.dtype).eval()
+        if fuse:   # q/k/v and gate/up as one GEMM each
+            fuse_projections(self.model)
         self.kv_caches: List[torch.Tensor] = []
         self.cpu_kv_caches: List[torch.Tensor] = []
         self._graphs: Dict[int, tuple] = {}

@@ -30,6 +30,7 @@ import torch
 from oracle import paged_ref
 from needle_amd import e2e
 from needle_amd.backend.request import SamplingParams
+from needle_amd.layers.attention import fused_outputs
 from needle_amd.model.config import QWEN2_0_5B, ModelConfig
 from needle_amd.model.qwen2 import build_model, random_init_
 
@@ -37,7 +38,8 @@ pytestmark = pytest.mark.gpu
 
 
 class Probe:
-    """Hooks that, while a graph is being captured, copy each layer's q/k/v projections and
+    """Hooks that, while a graph is being captured, copy each layer's q/k/v projections (the
+    layer's GEMM recomputed on its input) and
     attention output (o_proj's input) into tensors kept here; every replay rewrites them.
     Outside capture they do nothing."""
 
@@ -45,14 +47,18 @@ class Probe:
         self.store = {}
         for i, layer in enumerate(model.model.layers):
             att = layer.self_attn
-            for name in ("q_proj", "k_proj", "v_proj"):
-                getattr(att, name).register_forward_hook(self._after(i, name))
+            att.register_forward_pre_hook(self._projections(i, att))
             att.o_proj.register_forward_pre_hook(self._before(i))
 
-    def _after(self, i, name):
-        def hook(_mod, _inp, out):
+    def _projections(self, i, att):
+        # the layer's own projection GEMM (fused or not) on its input, run inside the capture
+        def hook(_mod, inp):
             if torch.cuda.is_current_stream_capturing():
-                self.store[(i, out.shape[0], name)] = out.clone()
+                x = inp[0]
+                outs = fused_outputs(att._qkv, (att.q_proj, att.k_proj, att.v_proj), x)
+                for name, out in zip(("q_proj", "k_proj", "v_proj"), outs):
+                    self.store[(i, x.shape[0], name)] = out.clone(
+                        memory_format=torch.contiguous_format)
         return hook
 
     def _before(self, i):

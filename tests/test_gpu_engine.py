@@ -30,6 +30,7 @@ from needle_amd.backend.request import SamplingParams, SeqState
 from needle_amd.backend.scheduler import Scheduler
 from needle_amd.model.config import QWEN2_0_5B, ModelConfig
 from needle_amd.model.runner import ModelRunner
+from needle_amd.layers.attention import fused_outputs
 from needle_amd.model.qwen2 import build_model, random_init_
 
 pytestmark = pytest.mark.gpu
@@ -112,7 +113,7 @@ class SeamCheck:
     """Checks every attention call of a GPU model against the oracle on the same inputs.
 
     Each layer's forward is wrapped: its q/k/v projections are recomputed on the GPU (the
-    same GEMMs), the pool is copied before the call, and after it the oracle runs on the
+    same GEMM the layer runs, fused or not), the pool is copied before the call, and after it the oracle runs on the
     host from those q/k/v, cos/sin, metadata and pool: RoPE as the reference's torch ops,
     then write_kv + per-sequence SDPA (prefill) or the decode append + _decode_pytorch.
     The layer's attention output (before o_proj) must be within the attention tolerance and
@@ -131,9 +132,11 @@ class SeamCheck:
         def forward(hidden_states, positions, kv_cache, block_table, cu_seqlens, context_lens,
                     max_seqlen, is_prefill, cos, sin):
             t = hidden_states.shape[0]
-            q = att.q_proj(hidden_states).view(t, att.num_heads, att.head_dim).cpu()
-            k = att.k_proj(hidden_states).view(t, att.num_kv_heads, att.head_dim).cpu()
-            v = att.v_proj(hidden_states).view(t, att.num_kv_heads, att.head_dim).cpu()
+            q, k, v = fused_outputs(att._qkv, (att.q_proj, att.k_proj, att.v_proj),
+                                    hidden_states)   # the layer's own GEMM(s)
+            q = q.reshape(t, att.num_heads, att.head_dim).cpu()
+            k = k.reshape(t, att.num_kv_heads, att.head_dim).cpu()
+            v = v.reshape(t, att.num_kv_heads, att.head_dim).cpu()
             pool = kv_cache.cpu()
             seen = {}
             attend = att._prefill_attend if is_prefill else att._decode_attend
