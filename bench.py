@@ -562,12 +562,22 @@ def llama_tp8_share(torch, ops, wl, reps):
                     "and every other collective are not part of it"}
 
 
+def progress(msg):
+    """A line on stderr as each part of the run ends (the JSON result stays alone on stdout)."""
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
 def extra_measurements(torch, ops, wl, reps, cpu_budget, cpu=True):
     """The other shapes, each with its CPU baseline (the reference torch path restated)."""
-    return {"qwen2_0.5b_decode": qwen05b_decode(torch, ops, wl, reps, cpu_budget, cpu=cpu),
-            "qwen2_7b_prefill": qwen7b_prefill(torch, ops, wl, reps, cpu=cpu),
-            "llama3_8b_long_context_decode": long_context_decode(torch, ops, wl, reps, cpu=cpu),
-            "llama3_8b_decode_tp8_share": llama_tp8_share(torch, ops, wl, reps)}
+    res = {"qwen2_0.5b_decode": qwen05b_decode(torch, ops, wl, reps, cpu_budget, cpu=cpu)}
+    progress("Qwen2-0.5B decode done")
+    res["qwen2_7b_prefill"] = qwen7b_prefill(torch, ops, wl, reps, cpu=cpu)
+    progress("Qwen2-7B prefill done")
+    res["llama3_8b_long_context_decode"] = long_context_decode(torch, ops, wl, reps, cpu=cpu)
+    progress("long-context decode done")
+    res["llama3_8b_decode_tp8_share"] = llama_tp8_share(torch, ops, wl, reps)
+    progress("tensor-parallel share done")
+    return res
 
 
 def ceilings(torch):
@@ -829,9 +839,11 @@ def main():
                       "algorithmic_bytes_per_launch": app_b,
                       "note": "64 rows per launch: latency-bound, not an HBM-bandwidth figure"},
     }
+    progress(f"headline step {ms_step:.4f} ms")
     cpu = not args.no_cpu_baseline
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(torch, wl, shape, ctx, args.cpu_seconds)
+        progress("CPU baseline done")
     if not args.no_extras:
         del pools
         torch.cuda.empty_cache()
@@ -839,8 +851,10 @@ def main():
                                                     cpu_budget=3.0, cpu=cpu)
     if not args.no_e2e:
         e2e_res = e2e_measurement(torch, args.e2e_seconds)
+        progress("end-to-end run done")
         if cpu:
             e2e_res["cpu_baseline"] = e2e_cpu_subset(torch)
+            progress("end-to-end CPU subset done")
         result.setdefault("other_shapes", {})["qwen2_0.5b_e2e_continuous_batching"] = e2e_res
     print(json.dumps(result), flush=True)
 
