@@ -23,6 +23,13 @@
  *   ndl_kv_block_copy   whole-block copies between pools for the KV swap
  *                       (needle/model/runner.py:175-192)
  *
+ * and the decoder layer's elementwise work on either side of the attention
+ * (needle/model/qwen2.py:52-65):
+ *
+ *   ndl_rms_norm        residual add + RMSNorm + weight product in one kernel
+ *                       (qwen2.py:58-63, needle/layers/norm.py:14-17)
+ *   ndl_silu_mul        silu(gate) * up of the SwiGLU MLP (needle/model/llama.py:36-37)
+ *
  * Conventions (every entry point):
  *   - Plain pointers to device memory, element counts and strides in ELEMENTS.
  *   - KV pool layout (needle/model/runner.py:65-78, attention.py:9-10):
@@ -52,7 +59,7 @@ extern "C" {
 /* Same object as hipStream_t; declared here so callers need no HIP headers. */
 typedef struct ihipStream_t* ndl_stream_t;
 
-#define NDL_ABI_VERSION 6
+#define NDL_ABI_VERSION 7
 
 enum ndl_status {
   NDL_OK = 0,
@@ -333,6 +340,43 @@ int ndl_kv_block_copy(void* const* dst_pools, int64_t dst_num_blocks,
                       int num_layers, int num_kv_heads, int block_size, int head_dim, int dtype,
                       const int32_t* src_ids, const int32_t* dst_ids, int num_pairs,
                       ndl_stream_t stream);
+
+/*
+ * RMSNorm of hidden-state rows, optionally after the residual add that precedes it.
+ *
+ * Replaces: needle/layers/norm.py:14-17 (RMSNorm.forward) and the residual adds of
+ *           needle/model/qwen2.py:58 and :63 that feed the next RMSNorm (the layer's
+ *           `residual + hidden_states`, then `residual = hidden_states` and the norm).
+ *
+ * residual == NULL:  out = weight * round(x * rsqrt(mean(x^2) + eps))
+ * residual != NULL:  h = round(x + residual) is written to residual_out (which may be
+ *                    residual itself), then out = weight * round(h * rsqrt(mean(h^2) + eps))
+ * with the reference's roundings: the statistic in fp32 (sum of squares times 1/hidden),
+ * the normalised value rounded to the dtype, the weight product rounded again.  x: rows of
+ * `hidden` elements, row stride x_row_stride (a multiple of 8, >= hidden); residual,
+ * residual_out, out: contiguous [rows][hidden]; weight: [hidden]; all in `dtype`, 16-byte
+ * aligned.  hidden: a multiple of 8, at most 8192 (NDL_ERR_UNSUPPORTED otherwise).
+ * out must not overlap x or residual.  rows == 0 is a no-op.
+ */
+int ndl_rms_norm(void* out, void* residual_out, const void* x, int64_t x_row_stride,
+                 const void* residual, const void* weight, int64_t rows, int hidden,
+                 float eps, int dtype, ndl_stream_t stream);
+
+/*
+ * The SwiGLU activation: out[r][i] = round(round(silu(gate[r][i])) * up[r][i]),
+ * silu(g) = g / (1 + exp(-g)) in fp32, rounded to the dtype as torch's silu is, then the
+ * product rounded again.
+ *
+ * Replaces: needle/model/llama.py:37 (F.silu(gate_proj(x)) * up_proj(x), two kernels).
+ *
+ * gate, up: rows of `intermediate` elements, row strides gate_row_stride / up_row_stride
+ * (multiples of 8; the halves of one fused gate/up projection output are gate = p,
+ * up = p + intermediate with both strides 2 * intermediate); out: contiguous
+ * [rows][intermediate]; 16-byte aligned; intermediate a multiple of 8.
+ */
+int ndl_silu_mul(void* out, const void* gate, int64_t gate_row_stride, const void* up,
+                 int64_t up_row_stride, int64_t rows, int intermediate, int dtype,
+                 ndl_stream_t stream);
 
 #ifdef __cplusplus
 }

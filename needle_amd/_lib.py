@@ -15,7 +15,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 _PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = _PKG_DIR / "libneedle_amd.so"
 
-NDL_ABI_VERSION = 6
+NDL_ABI_VERSION = 7
 NDL_DECODE_STATIC_SCRATCH_BYTES = 16 << 20
 NDL_DTYPE_BF16 = 0
 NDL_DTYPE_F16 = 1
@@ -35,6 +35,8 @@ EXPORTED_SYMBOLS = (
     "ndl_varlen_prefill",
     "ndl_rope_varlen_prefill",
     "ndl_kv_block_copy",
+    "ndl_rms_norm",
+    "ndl_silu_mul",
 )
 
 _c_i32 = ctypes.c_int
@@ -121,6 +123,15 @@ _SIGNATURES = {
         _c_p, _c_i64, _c_p, _c_i64,                     # dst pools, dst NB, src pools, src NB
         _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,         # layers, Hkv, bs, D, dtype
         _c_p, _c_p, _c_i32, _c_p,                       # src ids, dst ids, pairs, stream
+    ]),
+    "ndl_rms_norm": (_c_i32, [
+        _c_p, _c_p, _c_p, _c_i64,                       # out, residual out, x, x stride
+        _c_p, _c_p, _c_i64, _c_i32,                     # residual, weight, rows, hidden
+        _c_f32, _c_i32, _c_p,                           # eps, dtype, stream
+    ]),
+    "ndl_silu_mul": (_c_i32, [
+        _c_p, _c_p, _c_i64, _c_p, _c_i64,               # out, gate, stride, up, stride
+        _c_i64, _c_i32, _c_i32, _c_p,                   # rows, intermediate, dtype, stream
     ]),
 }
 

@@ -4,6 +4,9 @@ Structure and parameter names follow needle/model/qwen2.py:22-109 and
 needle/model/llama.py:18-140 of the reference:
   decoder layer = RMSNorm -> Attention (+residual) -> RMSNorm -> SwiGLU MLP (+residual)
   (qwen2.py:52-65); SwiGLU = down(silu(gate(x)) * up(x)) (llama.py:36-37);
+  each residual add is done by the RMSNorm that follows it (the next layer's input norm,
+  or the final norm), so a layer returns its MLP output and the residual stream apart
+  (the same values: the norm rounds x + residual to the dtype first, as the add did);
   Qwen2 adds biases to q/k/v (qwen2.py:22-39); the causal-LM head applies
   lm_head to the last token of each prefill sequence, or to every decode token
   (qwen2.py:100-109).
@@ -15,6 +18,7 @@ import torch
 import torch.nn as nn
 import torch.nn.functional as F
 
+from .. import ops
 from ..layers.attention import Attention, fuse_linears, fused_outputs
 from ..layers.norm import RMSNorm
 from ..layers.rope import RotaryEmbedding
@@ -35,6 +39,10 @@ class MLP(nn.Module):
 
     def forward(self, x):
         gate, up = fused_outputs(self._gate_up, (self.gate_proj, self.up_proj), x)
+        if x.is_cuda:   # one HIP kernel, torch's roundings
+            shape = gate.shape
+            act = ops.silu_mul(gate.reshape(-1, shape[-1]), up.reshape(-1, shape[-1]))
+            return self.down_proj(act.view(shape))
         return self.down_proj(F.silu(gate) * up)
 
 
@@ -47,15 +55,19 @@ class DecoderLayer(nn.Module):
         self.post_attention_layernorm = RMSNorm(config.hidden_size, eps=config.rms_norm_eps)
 
     def forward(self, hidden_states, positions, kv_cache, block_table, cu_seqlens, context_lens,
-                max_seqlen, is_prefill, cos, sin):
-        residual = hidden_states
-        h = self.input_layernorm(hidden_states)
+                max_seqlen, is_prefill, cos, sin, residual=None):
+        """Returns (MLP output, residual stream): the layer's output is their sum, which the
+        next RMSNorm forms (qwen2.py:58-65).  residual is None for the first layer, whose
+        input is the residual stream itself."""
+        if residual is None:
+            residual = hidden_states
+            h = self.input_layernorm(hidden_states)
+        else:
+            h, residual = self.input_layernorm(hidden_states, residual)
         h = self.self_attn(h, positions, kv_cache, block_table, cu_seqlens, context_lens,
                            max_seqlen, is_prefill, cos, sin)
-        h = residual + h
-        residual = h
-        h = self.post_attention_layernorm(h)
-        return residual + self.mlp(h)
+        h, residual = self.post_attention_layernorm(h, residual)
+        return self.mlp(h), residual
 
 
 class DecoderModel(nn.Module):
@@ -72,10 +84,11 @@ class DecoderModel(nn.Module):
                 max_seqlen, is_prefill):
         cos, sin = self.rotary_emb.get_cos_sin(positions)
         h = self.embed_tokens(input_ids)
+        residual = None
         for i, layer in enumerate(self.layers):
-            h = layer(h, positions, kv_caches[i], block_table, cu_seqlens, context_lens,
-                      max_seqlen, is_prefill, cos, sin)
-        return self.norm(h)
+            h, residual = layer(h, positions, kv_caches[i], block_table, cu_seqlens,
+                                context_lens, max_seqlen, is_prefill, cos, sin, residual)
+        return self.norm(h, residual)[0]
 
 
 class CausalLM(nn.Module):

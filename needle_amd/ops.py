@@ -1,7 +1,8 @@
 """torch-facing wrappers of the HIP paged-KV operations.
 
-Each function mirrors one seam of needle/layers/attention.py and forwards
-device pointers to the C ABI (include/needle_amd.h) on torch's current
+Each function mirrors one seam of needle/layers/attention.py (rms_norm and
+silu_mul: the decoder layer's elementwise ops around it, needle/model/qwen2.py:52-65)
+and forwards device pointers to the C ABI (include/needle_amd.h) on torch's current
 stream.  Nothing here computes on the host: the HIP library is required.
 
 Argument meaning follows the reference:
@@ -423,3 +424,69 @@ def kv_block_copy(dst_pools, src_pools, src_ids: torch.Tensor, dst_ids: torch.Te
                                _DTYPES[ref.dtype], src_ids.data_ptr(), dst_ids.data_ptr(), n,
                                _stream(dev))
     _lib.check(rc, "ndl_kv_block_copy")
+
+
+def _row_stride(name: str, x: torch.Tensor, width: int, dtype, device) -> int:
+    """Row stride of a [rows, width] tensor whose rows are contiguous and 16-byte aligned."""
+    _require(x.dim() == 2 and x.shape[1] == width, f"{name} must be [rows, {width}], "
+             f"got {tuple(x.shape)}")
+    _require(x.dtype == dtype, f"{name} must be {dtype}, got {x.dtype}", TypeError)
+    _require(x.device == device, f"{name} must be on {device}, got {x.device}")
+    _require(x.stride(1) == 1 or x.shape[1] == 1, f"{name} rows must be contiguous")
+    stride = x.stride(0) if x.shape[0] > 1 else width
+    _require(stride % 8 == 0 and x.data_ptr() % 16 == 0,
+             f"{name} rows must start 16-byte aligned (row stride {stride})")
+    return stride
+
+
+def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
+             residual: Optional[torch.Tensor] = None):
+    """RMSNorm of the rows of x (needle/layers/norm.py:14-17), in one kernel.
+
+    Without residual: returns weight * round(x * rsqrt(mean(x^2) + eps)).
+    With residual: h = round(x + residual) (the decoder layer's residual add,
+    needle/model/qwen2.py:58, :63) and returns (norm of h, h) as new tensors.
+    x: [rows, hidden] with contiguous rows; residual: [rows, hidden]; weight: [hidden];
+    one dtype (bfloat16, float16 or float32), on one GPU.
+    """
+    _require(x.is_cuda, "x must be a GPU tensor")
+    _require(x.dtype in _DTYPES, f"unsupported dtype {x.dtype}", TypeError)
+    rows, hidden = x.shape if x.dim() == 2 else (None, None)
+    _require(rows is not None, f"x must be [rows, hidden], got {tuple(x.shape)}")
+    stride = _row_stride("x", x, hidden, x.dtype, x.device)
+    _require(weight.shape == (hidden,) and weight.dtype == x.dtype and
+             weight.device == x.device and weight.is_contiguous(),
+             f"weight must be a contiguous [{hidden}] {x.dtype} tensor on {x.device}")
+    out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
+    res_out = None
+    if residual is not None:
+        _require(residual.shape == x.shape and residual.is_contiguous(),
+                 f"residual must be a contiguous {tuple(x.shape)} tensor")
+        _row_stride("residual", residual, hidden, x.dtype, x.device)
+        res_out = torch.empty_like(out)
+    lib = _lib.load()
+    rc = lib.ndl_rms_norm(out.data_ptr(), _ptr(res_out), x.data_ptr(), stride, _ptr(residual),
+                          weight.data_ptr(), rows, hidden, float(eps), _DTYPES[x.dtype],
+                          _stream(x.device))
+    _lib.check(rc, "ndl_rms_norm")
+    return out if residual is None else (out, res_out)
+
+
+def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """silu(gate) * up of the SwiGLU MLP (needle/model/llama.py:37), in one kernel, with
+    torch's roundings (the SiLU rounded to the dtype, then the product).  gate, up:
+    [rows, intermediate] with contiguous rows (e.g. the two halves of one fused gate/up
+    projection output); returns a new [rows, intermediate] tensor."""
+    _require(gate.is_cuda, "gate must be a GPU tensor")
+    _require(gate.dtype in _DTYPES, f"unsupported dtype {gate.dtype}", TypeError)
+    _require(gate.dim() == 2, f"gate must be [rows, intermediate], got {tuple(gate.shape)}")
+    rows, inter = gate.shape
+    gs = _row_stride("gate", gate, inter, gate.dtype, gate.device)
+    us = _row_stride("up", up, inter, gate.dtype, gate.device)
+    _require(up.shape[0] == rows, f"up has {up.shape[0]} rows, gate {rows}")
+    out = torch.empty((rows, inter), dtype=gate.dtype, device=gate.device)
+    lib = _lib.load()
+    rc = lib.ndl_silu_mul(out.data_ptr(), gate.data_ptr(), gs, up.data_ptr(), us, rows, inter,
+                          _DTYPES[gate.dtype], _stream(gate.device))
+    _lib.check(rc, "ndl_silu_mul")
+    return out
