@@ -29,6 +29,8 @@
  *   ndl_rms_norm        residual add + RMSNorm + weight product in one kernel
  *                       (qwen2.py:58-63, needle/layers/norm.py:14-17)
  *   ndl_silu_mul        silu(gate) * up of the SwiGLU MLP (needle/model/llama.py:36-37)
+ *   ndl_greedy_argmax   the greedy sampler's argmax for a batch of logit rows
+ *                       (needle/model/sampler.py:27-28)
  *
  * Conventions (every entry point):
  *   - Plain pointers to device memory, element counts and strides in ELEMENTS.
@@ -377,6 +379,21 @@ int ndl_rms_norm(void* out, void* residual_out, const void* x, int64_t x_row_str
 int ndl_silu_mul(void* out, const void* gate, int64_t gate_row_stride, const void* up,
                  int64_t up_row_stride, int64_t rows, int intermediate, int dtype,
                  ndl_stream_t stream);
+
+/*
+ * Greedy sampling: out[r] = the index of the maximum of logits row r, in torch's argmax
+ * order (a NaN is larger than every number and the first NaN wins; of equal maxima the
+ * lowest index wins).
+ *
+ * Replaces: needle/model/sampler.py:27-28 (int(logit.argmax()) per greedy row, each with a
+ *           host sync), for every row of the batch in one launch.
+ *
+ * logits: rows of `vocab` elements in `dtype`, row stride row_stride (a multiple of 8,
+ * >= vocab), 16-byte aligned.  out: int32 [rows] (out_is_int64 = 0) or int64 [rows].
+ * Records no memset or allocation, so it can be captured in a HIP graph.
+ */
+int ndl_greedy_argmax(void* out, int out_is_int64, const void* logits, int64_t row_stride,
+                      int64_t rows, int vocab, int dtype, ndl_stream_t stream);
 
 #ifdef __cplusplus
 }

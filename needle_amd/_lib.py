@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "ndl_kv_block_copy",
     "ndl_rms_norm",
     "ndl_silu_mul",
+    "ndl_greedy_argmax",
 )
 
 _c_i32 = ctypes.c_int
@@ -132,6 +133,10 @@ _SIGNATURES = {
     "ndl_silu_mul": (_c_i32, [
         _c_p, _c_p, _c_i64, _c_p, _c_i64,               # out, gate, stride, up, stride
         _c_i64, _c_i32, _c_i32, _c_p,                   # rows, intermediate, dtype, stream
+    ]),
+    "ndl_greedy_argmax": (_c_i32, [
+        _c_p, _c_i32, _c_p, _c_i64,                     # out, out int64, logits, stride
+        _c_i64, _c_i32, _c_i32, _c_p,                   # rows, vocab, dtype, stream
     ]),
 }
 

@@ -439,12 +439,14 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
         // st[i] is the score of token tix*16 + 4j + i for head c.
         const int pos0 = tix * 16 + 4 * j;
         const bool partial = t.bad || (tix * 16 + 16 > t1);  // wave-uniform
+        // This lane's tokens pos0 + i are attended for i < lim: all four in a full tile of
+        // a valid block, none in an invalid one.  (A select per score, no branches.)
+        const int lim = t.bad ? 0 : t1 - pos0;
         float sc[4];
         float mt = kNegInf;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const bool ok = !partial || (!t.bad && pos0 + i < t1);
-          sc[i] = ok ? st[i] * a.scale_log2 : kNegInf;
+          sc[i] = i < lim ? st[i] * a.scale_log2 : kNegInf;
           mt = fmaxf(mt, sc[i]);
         }
         mt = max_xor32(max_xor16(mt));
@@ -467,10 +469,8 @@ __global__ __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(
 
         if (partial) {  // masked rows may hold stale bits (NaN * 0 = NaN): clear them
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool ok = !t.bad && pos0 + i < t1;
-            if (!ok) t.v[i] = VT{};
-          }
+          for (int i = 0; i < 4; ++i)
+            if (i >= lim) t.v[i] = VT{};
         }
 
         const u32x2 pb = {T::pack(p[0], p[1]), T::pack(p[2], p[3])};

@@ -332,13 +332,15 @@ class ModelRunner:
         torch.cuda.synchronize(self.device)
 
     def _decode_body(self, b: int) -> torch.Tensor:
-        """The captured decode step of the first b rows (the forward only: torch's argmax
-        over a vocabulary row can split into a multi-workgroup reduction that clears its
-        semaphores with a memset, which a graph must not record)."""
+        """The captured decode step of the first b rows: the forward, then the greedy
+        argmax of every row (ndl_greedy_argmax, which records no memset), written into the
+        rows' input tokens for the next step."""
         rows = self._rows
         ctx = rows.ctx[:b]
-        return self.model(rows.tok[:b], ctx.long(), self.kv_caches, rows.table[:b],
-                          self._cu[:b + 1], ctx, 1, False)
+        logits = self.model(rows.tok[:b], ctx.long(), self.kv_caches, rows.table[:b],
+                            self._cu[:b + 1], ctx, 1, False)
+        ops.greedy_argmax(logits, out=rows.tok[:b])
+        return logits
 
     def _graph_decode(self, seqs: List[SeqState]) -> Optional[List[int]]:
         rows = self._rows
@@ -351,11 +353,9 @@ class ModelRunner:
         if bucket is None:
             return None
         rows.sync(seqs)
-        g, logits = self._graphs[bucket]
-        g.replay()
-        nxt = torch.argmax(logits[:b], dim=-1)
-        rows.tok[:b].copy_(nxt)                  # the next step's input ids stay on the device
-        greedy = nxt.tolist()                    # one host copy (row order)
+        g, _ = self._graphs[bucket]
+        g.replay()                               # the next step's input ids stay on the device
+        greedy = rows.tok[:b].tolist()           # one host copy (row order)
         where = rows.row_of()
         order = [where[id(s)] for s in seqs]
         out = [greedy[r] for r in order]

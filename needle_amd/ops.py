@@ -490,3 +490,26 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
                           _DTYPES[gate.dtype], _stream(gate.device))
     _lib.check(rc, "ndl_silu_mul")
     return out
+
+
+def greedy_argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The index of each row's maximum, in torch's argmax order (needle/model/sampler.py:
+    27-28, for the whole batch in one launch).  logits: [rows, vocab] with contiguous,
+    16-byte aligned rows; out: int32 or int64 [rows] on the same GPU (a new int64 tensor by
+    default).  Graph-capturable."""
+    _require(logits.is_cuda, "logits must be a GPU tensor")
+    _require(logits.dtype in _DTYPES, f"unsupported dtype {logits.dtype}", TypeError)
+    _require(logits.dim() == 2, f"logits must be [rows, vocab], got {tuple(logits.shape)}")
+    rows, vocab = logits.shape
+    stride = _row_stride("logits", logits, vocab, logits.dtype, logits.device)
+    if out is None:
+        out = torch.empty(rows, dtype=torch.int64, device=logits.device)
+    _require(out.dtype in (torch.int32, torch.int64) and out.shape == (rows,) and
+             out.is_contiguous() and out.device == logits.device,
+             f"out must be a contiguous int32 or int64 [{rows}] tensor on {logits.device}")
+    lib = _lib.load()
+    rc = lib.ndl_greedy_argmax(out.data_ptr(), int(out.dtype == torch.int64),
+                               logits.data_ptr(), stride, rows, vocab, _DTYPES[logits.dtype],
+                               _stream(logits.device))
+    _lib.check(rc, "ndl_greedy_argmax")
+    return out

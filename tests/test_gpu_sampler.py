@@ -1,0 +1,111 @@
+"""Greedy sampling on the GPU (ndl_greedy_argmax) against torch's argmax.
+
+Reference: needle/model/sampler.py:27-28 (int(logit.argmax()) per greedy row).  The kernel
+must return torch's index exactly: the first of equal maxima, a NaN above every number (the
+first NaN), -0 equal to +0.  Cases: random rows of the real vocabulary (151,936), rows drawn
+from a handful of values (ties everywhere, the common case of flat bf16 logits), NaN and
+-inf rows, a vocabulary that is not a multiple of 8 read through a wider row stride, every
+dtype, int32 and int64 outputs, and the launch recorded in a HIP graph and replayed with
+eager work in between.
+"""
+import pytest
+import torch
+
+from needle_amd import ops
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+def _want(logits):
+    return logits.float().cpu().argmax(dim=-1)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("rows,vocab", [(1, 151936), (48, 151936), (256, 151936), (3, 8),
+                                        (5, 1000)])
+def test_argmax_random_rows(dtype, rows, vocab):
+    g = torch.Generator().manual_seed(rows * 7 + vocab)
+    logits = (torch.randn(rows, vocab, generator=g) * 3).to(dtype).to(DEV)
+    got = ops.greedy_argmax(logits)
+    assert got.dtype == torch.int64
+    assert torch.equal(got.cpu(), _want(logits))
+    assert torch.equal(got.cpu(), logits.argmax(dim=-1).cpu())   # torch on the same GPU
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_argmax_ties_take_the_first_index(dtype):
+    g = torch.Generator().manual_seed(5)
+    vals = torch.tensor([-2.0, -0.0, 0.0, 1.5, 3.0])
+    logits = vals[torch.randint(0, 5, (64, 151936), generator=g)].to(dtype).to(DEV)
+    logits[7] = 0.0
+    logits[8] = -0.0
+    logits[8, 50] = 0.0                                       # -0 and +0 tie: index 0
+    logits[9] = -2.0
+    logits[9, 151935] = 3.0                                   # the last entry
+    out32 = torch.empty(64, dtype=torch.int32, device=DEV)
+    got = ops.greedy_argmax(logits, out=out32)
+    assert got is out32
+    want = _want(logits)
+    assert torch.equal(got.cpu().long(), want)
+    assert want[7] == 0 and want[8] == 0 and want[9] == 151935
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_argmax_nan_and_inf_rows(dtype):
+    logits = torch.zeros(6, 4096, dtype=dtype, device=DEV)
+    logits[0, 17] = float("nan")
+    logits[0, 3000] = float("inf")                            # NaN beats +inf
+    logits[1, 5] = float("nan")
+    logits[1, 4] = float("nan")                               # the first NaN
+    logits[2] = float("-inf")                                 # all -inf: index 0
+    logits[3, 2000] = float("inf")
+    logits[3, 1000] = float("inf")
+    logits[4] = float("-inf")
+    logits[4, 4095] = -1e4
+    logits[5, 9] = float("nan")
+    logits[5, 10] = float("inf")
+    got = ops.greedy_argmax(logits).cpu()
+    assert got.tolist() == [17, 4, 0, 1000, 4095, 9]
+    assert torch.equal(got, logits.argmax(dim=-1).cpu())
+
+
+def test_argmax_strided_rows_and_tail():
+    g = torch.Generator().manual_seed(11)
+    wide = torch.randn(9, 1008, generator=g).to(torch.bfloat16).to(DEV)
+    wide[:, 1003] = 100.0                                     # outside the view: ignored
+    view = wide[:, :1003]                                     # vocab % 8 == 3, stride 1008
+    view[4, 1001] = 50.0                                      # inside the tail
+    got = ops.greedy_argmax(view)
+    assert torch.equal(got.cpu(), _want(view))
+    assert got[4].item() == 1001
+
+
+def test_argmax_in_a_graph():
+    g = torch.Generator().manual_seed(3)
+    logits = torch.randn(32, 151936, generator=g).to(torch.bfloat16).to(DEV)
+    out = torch.zeros(32, dtype=torch.int32, device=DEV)
+    ops.greedy_argmax(logits, out=out)                        # warm-up outside the capture
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.greedy_argmax(logits, out=out)
+    for i in range(4):
+        logits.copy_(torch.randn(32, 151936, generator=g).to(torch.bfloat16))
+        out.fill_(-1)                                         # eager work between replays
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.cpu().long(), _want(logits)), f"replay {i}"
+
+
+def test_argmax_rejects_bad_arguments():
+    from needle_amd._lib import NeedleAmdError
+    logits = torch.zeros(4, 100, dtype=torch.bfloat16, device=DEV)
+    with pytest.raises((ValueError, NeedleAmdError)):          # row stride not a multiple of 8
+        ops.greedy_argmax(logits)
+    with pytest.raises(ValueError):
+        ops.greedy_argmax(torch.zeros(4, 104, dtype=torch.bfloat16, device=DEV),
+                          out=torch.zeros(3, dtype=torch.int64, device=DEV))
+    assert ops.greedy_argmax(torch.zeros(0, 104, dtype=torch.bfloat16, device=DEV)).numel() == 0
