@@ -51,30 +51,45 @@ __global__ __launch_bounds__(kArgThreads) void greedy_argmax_kernel(ArgmaxArgs a
   float bv = kNegInf;
   int bi = 0x7fffffff;
   const int chunks = a.vocab / 8;
-  for (int ch = threadIdx.x; ch < chunks; ch += kArgThreads) {
-    float v[8];
-    if constexpr (FMT == kFmtF32) {
-      const u32x4 p = ld16(row + ch * 32), q = ld16(row + ch * 32 + 16);
+  // kBatch chunks per thread are loaded before any is compared, so that many loads are in
+  // flight at once; a chunk past the row is not loaded and not compared.
+  constexpr int kBatch = FMT == kFmtF32 ? 4 : 8;
+  constexpr int CW = FMT == kFmtF32 ? 2 : 1;   // 16-byte words per chunk
+  for (int ch0 = threadIdx.x; ch0 < chunks; ch0 += kBatch * kArgThreads) {
+    u32x4 p[kBatch][CW];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[e] = __uint_as_float(p[e]);
-        v[4 + e] = __uint_as_float(q[e]);
-      }
-    } else {
-      using T = Elt<FMT == kFmtF16>;
-      const u32x4 p = ld16(row + ch * 16);
+    for (int u = 0; u < kBatch; ++u) {
+      const int ch = ch0 + u * kArgThreads;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        v[2 * e] = T::lo(p[e]);
-        v[2 * e + 1] = T::hi(p[e]);
-      }
+      for (int w = 0; w < CW; ++w)
+        p[u][w] = ch < chunks ? ld16(row + (ch * CW + w) * 16) : u32x4{0u, 0u, 0u, 0u};
     }
 #pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (better(v[e], 8 * ch + e, bv, bi)) {
-        bv = v[e];
-        bi = 8 * ch + e;
+    for (int u = 0; u < kBatch; ++u) {
+      const int ch = ch0 + u * kArgThreads;
+      if (ch >= chunks) break;
+      float v[8];
+      if constexpr (FMT == kFmtF32) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[e] = __uint_as_float(p[u][0][e]);
+          v[4 + e] = __uint_as_float(p[u][1][e]);
+        }
+      } else {
+        using T = Elt<FMT == kFmtF16>;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          v[2 * e] = T::lo(p[u][0][e]);
+          v[2 * e + 1] = T::hi(p[u][0][e]);
+        }
       }
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (better(v[e], 8 * ch + e, bv, bi)) {
+          bv = v[e];
+          bi = 8 * ch + e;
+        }
+    }
   }
   // the vocab % 8 last entries
   for (int i = 8 * chunks + (int)threadIdx.x; i < a.vocab; i += kArgThreads) {

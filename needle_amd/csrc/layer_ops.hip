@@ -91,8 +91,9 @@ struct NormArgs {
   float eps, inv_hidden;
 };
 
-// One wave per row; lane l holds chunks l, l + 64, .. (8 elements each) of the row in
-// registers between the statistic and the products.
+// One wave per row; lane l holds chunks l, l + 64, .. (8 elements each) of the row, and the
+// same chunks of the weight (loaded with the row: one memory round trip), in registers
+// between the statistic and the products.
 template <int FMT, int NC, bool RES>
 __global__ __launch_bounds__(kThreads) void rms_norm_kernel(NormArgs a) {
   constexpr int EB = FMT == kFmtF32 ? 4 : 2;
@@ -102,13 +103,14 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(NormArgs a) {
   const int chunks = a.hidden / 8;
   const char* x = static_cast<const char*>(a.x) + row * a.x_stride * EB;
   const int64_t row_off = row * a.hidden * EB;
-  float h[NC][8];
+  float h[NC][8], w[NC][8];
   float ss = 0.f;
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int ch = lane + 64 * c;
     if (ch >= chunks) continue;
     load8<FMT>(x + ch * 8 * EB, h[c]);
+    load8<FMT>(static_cast<const char*>(a.weight) + ch * 8 * EB, w[c]);
     if constexpr (RES) {
       float r[8];
       load8<FMT>(static_cast<const char*>(a.residual) + row_off + ch * 8 * EB, r);
@@ -125,11 +127,10 @@ __global__ __launch_bounds__(kThreads) void rms_norm_kernel(NormArgs a) {
   for (int c = 0; c < NC; ++c) {
     const int ch = lane + 64 * c;
     if (ch >= chunks) continue;
-    float w[8], o[8];
-    load8<FMT>(static_cast<const char*>(a.weight) + ch * 8 * EB, w);
+    float o[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e)
-      o[e] = round_to<FMT>(__fmul_rn(w[e], round_to<FMT>(__fmul_rn(h[c][e], rstd))));
+      o[e] = round_to<FMT>(__fmul_rn(w[c][e], round_to<FMT>(__fmul_rn(h[c][e], rstd))));
     store8<FMT>(static_cast<char*>(a.out) + row_off + ch * 8 * EB, o);
   }
 }
