@@ -47,8 +47,11 @@
 
 namespace ndl {
 
-// The fewest tiles a wave of the automatic split takes.
-constexpr int kDecodeMinChunk = 2;
+// The fewest tiles a wave of the automatic split takes: shorter pieces cost more in
+// partials and merge work than their parallelism gains (Llama-3-8B decode at one GPU's
+// share of 8-way tensor parallelism, 1 kv head, ~4.4 tiles per resident wave: 25.4 us per
+// layer at 5 tiles per wave, 23.3 at 8; shares with longer even splits are unchanged).
+constexpr int kDecodeMinChunk = 8;
 // Waves per workgroup of the per-sequence split, and the most tiles per wave for which
 // the automatic choice takes it (a table of up to 256 columns at head_dim 64, 128 at
 // 128).  Eight waves (two per SIMD) measured faster than sixteen (four per SIMD) at
