@@ -7,7 +7,7 @@ and its decoder layer adds the residual before each norm (needle/model/qwen2.py:
 On the GPU, forward(x, residual) is one HIP kernel (ndl_rms_norm: the add, the statistic,
 the two products, with the same roundings); only the order of the fp32 sum of squares
 differs from torch's reduction, which moves an element by an ulp of its format now and
-then (tests/test_norm.py).  On the CPU (the oracle runner of the tests and the CPU
+then (tests/test_layer_ops.py).  On the CPU (the oracle runner of the tests and the CPU
 baseline) it is torch's fused RMS normalisation without a weight followed by the weight
 product: the same bits as the reference's op sequence.
 """
