@@ -451,8 +451,8 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     """
     _require(x.is_cuda, "x must be a GPU tensor")
     _require(x.dtype in _DTYPES, f"unsupported dtype {x.dtype}", TypeError)
-    rows, hidden = x.shape if x.dim() == 2 else (None, None)
-    _require(rows is not None, f"x must be [rows, hidden], got {tuple(x.shape)}")
+    _require(x.dim() == 2, f"x must be [rows, hidden], got {tuple(x.shape)}")
+    rows, hidden = x.shape
     stride = _row_stride("x", x, hidden, x.dtype, x.device)
     _require(weight.shape == (hidden,) and weight.dtype == x.dtype and
              weight.device == x.device and weight.is_contiguous(),
