@@ -79,7 +79,9 @@ class _DecodeRows:
         self.dirty: List[bool] = []          # row refilled: send all of it
         self.tok_on_device: List[bool] = []  # the graph wrote this row's newest token
         self._staging: List[torch.Tensor] = []
-        self._events = [None, None]
+        self._staging_np: list = []
+        self._events: list = [None, None]
+        self._recorded = [False, False]
         self._turn = 0
         self._dev_pairs = torch.empty(0, dtype=torch.int32, device=device)
 
@@ -157,22 +159,22 @@ class _DecodeRows:
             size = max(8192, 4 * n)
             self._staging = [torch.empty(size, dtype=torch.int32).pin_memory()
                              for _ in range(2)]
-            self._events = [None, None]
+            self._staging_np = [h.numpy() for h in self._staging]
+            self._events = [torch.cuda.Event(), torch.cuda.Event()]
+            self._recorded = [False, False]
             self._dev_pairs = torch.empty(size, dtype=torch.int32, device=self.meta.device)
         t = self._turn
         self._turn ^= 1
-        if self._events[t] is not None:
+        if self._recorded[t]:
             self._events[t].synchronize()        # the copy that last read this buffer
-        host = self._staging[t]
-        arr = host.numpy()
+        arr = self._staging_np[t]
         arr[:n] = idx
         arr[n:2 * n] = val
         dev = self._dev_pairs[:2 * n]
-        dev.copy_(host[:2 * n], non_blocking=True)
-        ev = torch.cuda.Event()
-        ev.record()
-        self._events[t] = ev
-        self.meta.index_put_((dev[:n].long(),), dev[n:2 * n])
+        dev.copy_(self._staging[t][:2 * n], non_blocking=True)
+        self._events[t].record()
+        self._recorded[t] = True
+        self.meta.index_put_((dev[:n],), dev[n:2 * n])   # int32 indices: no widening kernel
 
     def row_of(self) -> Dict[int, int]:
         return {id(s): r for r, s in enumerate(self.rows)}
