@@ -61,7 +61,7 @@ extern "C" {
 /* Same object as hipStream_t; declared here so callers need no HIP headers. */
 typedef struct ihipStream_t* ndl_stream_t;
 
-#define NDL_ABI_VERSION 7
+#define NDL_ABI_VERSION 8
 
 enum ndl_status {
   NDL_OK = 0,
@@ -386,14 +386,20 @@ int ndl_silu_mul(void* out, const void* gate, int64_t gate_row_stride, const voi
  * lowest index wins).
  *
  * Replaces: needle/model/sampler.py:27-28 (int(logit.argmax()) per greedy row, each with a
- *           host sync), for every row of the batch in one launch.
+ *           host sync), for every row of the batch.
  *
  * logits: rows of `vocab` elements in `dtype`, row stride row_stride (a multiple of 8,
- * >= vocab), 16-byte aligned.  out: int32 [rows] (out_is_int64 = 0) or int64 [rows].
- * Records no memset or allocation, so it can be captured in a HIP graph.
+ * >= vocab), 16-byte aligned; rows <= 65535.  out: int32 [rows] (out_is_int64 = 0) or int64
+ * [rows].  Long rows are scanned in slices by several workgroups whose partial results go
+ * to `workspace` (ndl_greedy_argmax_workspace_bytes(rows, vocab) bytes, 4-byte aligned; 0
+ * when one slice per row suffices, then workspace may be NULL), then a second launch picks
+ * each row's best.  Calls that share a workspace must be ordered (one stream).  Records no
+ * memset or allocation, so it can be captured in a HIP graph.
  */
+size_t ndl_greedy_argmax_workspace_bytes(int64_t rows, int vocab);
 int ndl_greedy_argmax(void* out, int out_is_int64, const void* logits, int64_t row_stride,
-                      int64_t rows, int vocab, int dtype, ndl_stream_t stream);
+                      int64_t rows, int vocab, int dtype, void* workspace,
+                      size_t workspace_bytes, ndl_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -15,7 +15,7 @@ import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 _PKG_DIR = Path(__file__).resolve().parent
 LIB_PATH = _PKG_DIR / "libneedle_amd.so"
 
-NDL_ABI_VERSION = 7
+NDL_ABI_VERSION = 8
 NDL_DECODE_STATIC_SCRATCH_BYTES = 16 << 20
 NDL_DTYPE_BF16 = 0
 NDL_DTYPE_F16 = 1
@@ -37,6 +37,7 @@ EXPORTED_SYMBOLS = (
     "ndl_kv_block_copy",
     "ndl_rms_norm",
     "ndl_silu_mul",
+    "ndl_greedy_argmax_workspace_bytes",
     "ndl_greedy_argmax",
 )
 
@@ -134,9 +135,11 @@ _SIGNATURES = {
         _c_p, _c_p, _c_i64, _c_p, _c_i64,               # out, gate, stride, up, stride
         _c_i64, _c_i32, _c_i32, _c_p,                   # rows, intermediate, dtype, stream
     ]),
+    "ndl_greedy_argmax_workspace_bytes": (_c_sz, [_c_i64, _c_i32]),   # rows, vocab
     "ndl_greedy_argmax": (_c_i32, [
         _c_p, _c_i32, _c_p, _c_i64,                     # out, out int64, logits, stride
-        _c_i64, _c_i32, _c_i32, _c_p,                   # rows, vocab, dtype, stream
+        _c_i64, _c_i32, _c_i32,                         # rows, vocab, dtype
+        _c_p, _c_sz, _c_p,                              # workspace, bytes, stream
     ]),
 }
 

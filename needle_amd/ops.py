@@ -494,7 +494,8 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
 
 def greedy_argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The index of each row's maximum, in torch's argmax order (needle/model/sampler.py:
-    27-28, for the whole batch in one launch).  logits: [rows, vocab] with contiguous,
+    27-28, for the whole batch: one or two launches, the slices' partials in a workspace
+    allocated here, from the graph's pool under capture).  logits: [rows, vocab] with contiguous,
     16-byte aligned rows; out: int32 or int64 [rows] on the same GPU (a new int64 tensor by
     default).  Graph-capturable."""
     _require(logits.is_cuda, "logits must be a GPU tensor")
@@ -508,8 +509,10 @@ def greedy_argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> t
              out.is_contiguous() and out.device == logits.device,
              f"out must be a contiguous int32 or int64 [{rows}] tensor on {logits.device}")
     lib = _lib.load()
+    nbytes = lib.ndl_greedy_argmax_workspace_bytes(rows, vocab) if rows > 0 else 0
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device) if nbytes else None
     rc = lib.ndl_greedy_argmax(out.data_ptr(), int(out.dtype == torch.int64),
                                logits.data_ptr(), stride, rows, vocab, _DTYPES[logits.dtype],
-                               _stream(logits.device))
+                               _ptr(ws), nbytes, _stream(logits.device))
     _lib.check(rc, "ndl_greedy_argmax")
     return out

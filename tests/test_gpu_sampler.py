@@ -5,8 +5,9 @@ must return torch's index exactly: the first of equal maxima, a NaN above every 
 first NaN), -0 equal to +0.  Cases: random rows of the real vocabulary (151,936), rows drawn
 from a handful of values (ties everywhere, the common case of flat bf16 logits), NaN and
 -inf rows, a vocabulary that is not a multiple of 8 read through a wider row stride, every
-dtype, int32 and int64 outputs, and the launch recorded in a HIP graph and replayed with
-eager work in between.
+dtype, int32 and int64 outputs, rows scanned in one slice or several (ties across a slice
+edge), the workspace check, and the launches recorded in a HIP graph and replayed with eager
+work in between.
 """
 import pytest
 import torch
@@ -109,3 +110,45 @@ def test_argmax_rejects_bad_arguments():
         ops.greedy_argmax(torch.zeros(4, 104, dtype=torch.bfloat16, device=DEV),
                           out=torch.zeros(3, dtype=torch.int64, device=DEV))
     assert ops.greedy_argmax(torch.zeros(0, 104, dtype=torch.bfloat16, device=DEV)).numel() == 0
+
+
+@pytest.mark.parametrize("rows,vocab", [(1, 600000), (3, 151936), (600, 151936), (2, 8200),
+                                        (17, 16384)])
+def test_argmax_slices(rows, vocab):
+    """One slice per row (many rows), several (few rows, long rows, up to the 64-slice cap),
+    slices ending inside the last 8-element chunk."""
+    from needle_amd import _lib
+    g = torch.Generator().manual_seed(rows + vocab)
+    logits = torch.randn(rows, vocab, generator=g).to(torch.bfloat16).to(DEV)
+    logits[0, vocab - 1] = 50.0                               # the very last entry
+    if rows > 1:
+        logits[1, 8191] = 60.0                                # at a slice edge
+        logits[1, 8192] = 60.0                                # tie across it: the first wins
+    got = ops.greedy_argmax(logits)
+    assert torch.equal(got.cpu(), _want(logits))
+    lib = _lib.load()
+    print(f"rows {rows} vocab {vocab}: workspace "
+          f"{lib.ndl_greedy_argmax_workspace_bytes(rows, vocab)} bytes")
+
+
+def test_argmax_workspace_too_small_is_refused():
+    import ctypes
+    from needle_amd import _lib
+    lib = _lib.load()
+    logits = torch.zeros(2, 151936, dtype=torch.bfloat16, device=DEV)
+    out = torch.zeros(2, dtype=torch.int64, device=DEV)
+    need = lib.ndl_greedy_argmax_workspace_bytes(2, 151936)
+    assert need > 0
+    ws = torch.empty(need, dtype=torch.uint8, device=DEV)
+    st = torch.cuda.current_stream().cuda_stream
+    rc = lib.ndl_greedy_argmax(out.data_ptr(), 1, logits.data_ptr(), 151936, 2, 151936,
+                               _lib.NDL_DTYPE_BF16, ws.data_ptr(), need - 8, st)
+    assert rc == -3                                           # NDL_ERR_WORKSPACE
+    rc = lib.ndl_greedy_argmax(out.data_ptr(), 1, logits.data_ptr(), 151936, 2, 151936,
+                               _lib.NDL_DTYPE_BF16, None, 0, st)
+    assert rc == -3
+    rc = lib.ndl_greedy_argmax(out.data_ptr(), 1, logits.data_ptr(), 151936, 2, 151936,
+                               _lib.NDL_DTYPE_BF16, ws.data_ptr(), need, st)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert out.tolist() == [0, 0]
