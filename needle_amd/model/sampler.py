@@ -1,8 +1,8 @@
 """Next-token sampling (reference needle/model/sampler.py:16-46), greedy only.
 
 Greedy rows (temperature 0) take the argmax of the logits (sampler.py:27-28), computed for
-the whole batch on the device in one launch (ndl_greedy_argmax, torch's argmax order) and
-copied to the host once; on the CPU, torch's argmax.  Temperature, top-k and top-p sampling are outside
+the whole batch on the device (ndl_greedy_argmax, torch's argmax order) and copied to the
+host once; on the CPU, torch's argmax.  Temperature, top-k and top-p sampling are outside
 the paged-KV path this package rebuilds; a request that asks for them is refused
 (LLMEngine.add_request raises before it is queued, and this function raises too).
 """
@@ -29,5 +29,5 @@ def sample(logits: torch.Tensor, params: List[SamplingParams]) -> List[int]:
     for p in params:
         check_greedy(p)
     if logits.is_cuda:
-        return ops.greedy_argmax(logits).tolist()  # one launch, one host copy for the batch
+        return ops.greedy_argmax(logits).tolist()  # the whole batch, one host copy
     return logits.argmax(dim=-1).tolist()
