@@ -1,8 +1,8 @@
 """CPU oracle of Needle's paged-KV hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may use
-this package, and only as the checker (or as the timed CPU baseline).  The
-product path (needle_amd) never imports it.
+this package, and only as the reference results are compared against (or as the
+timed CPU baseline).  The product path (needle_amd) never imports it.
 
 Contents (each function cites the reference file:line it restates):
   paged_ref.slot_of_tokens   integer slot rule      attention.py:141-146, 217-237
