@@ -183,7 +183,7 @@ def test_benchmark_engine_graph_replays_match_eager_and_the_oracle():
     probe = Probe(model)
     engine = e2e.build_engine(model=model)
     assert engine.runner._rows.width == 96 and max(engine.runner._graphs) == 256
-    checker = CheckedReplays(engine, probe, oracle_buckets=(8, 48))
+    checked = CheckedReplays(engine, probe, oracle_buckets=(8, 48))
 
     bench = e2e.requests(8)
     for i, (rid, prompt, _olen) in enumerate(bench):
@@ -203,9 +203,9 @@ def test_benchmark_engine_graph_replays_match_eager_and_the_oracle():
         steps += 1
         assert steps < 200
     assert len(done) == 48
-    seen = sorted(checker.replays)
-    print(f"benchmark engine: {steps} steps, replays per bucket {checker.replays}, worst "
-          f"|graph - eager| {checker.worst:.3g}, oracle checks {checker.oracle_checked}",
+    seen = sorted(checked.replays)
+    print(f"benchmark engine: {steps} steps, replays per bucket {checked.replays}, worst "
+          f"|graph - eager| {checked.worst:.3g}, oracle checks {checked.oracle_checked}",
           flush=True)
     assert 8 in seen and 48 in seen and len(seen) >= 4
-    assert [c[0] for c in checker.oracle_checked] == [8, 48]
+    assert [c[0] for c in checked.oracle_checked] == [8, 48]
