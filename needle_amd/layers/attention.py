@@ -67,14 +67,19 @@ def _still_fused(fused, mods) -> bool:
     """True while every layer's weight (and bias) is the view fuse_linears made of the fused
     tensor (a later .to() or a replaced parameter gives it storage of its own)."""
     w, b = fused
+    # Row r0 of the fused tensor starts r0 * stride(0) elements in; comparing addresses that
+    # way avoids building a slice per layer on every forward.
+    wp, ws, dev = w.data_ptr(), w.stride(0) * w.element_size(), w.device
+    bp, bs = (b.data_ptr(), b.element_size()) if b is not None else (0, 0)
     r0 = 0
     for m in mods:
-        r = m.weight.shape[0]
-        if m.weight.data_ptr() != w[r0:r0 + r].data_ptr() or m.weight.device != w.device:
+        p = m._parameters  # the dict nn.Module.__getattr__ would search, read once
+        mw, mb = p["weight"], p.get("bias")
+        if mw.data_ptr() != wp + r0 * ws or mw.device != dev:
             return False
-        if b is not None and (m.bias is None or m.bias.data_ptr() != b[r0:r0 + r].data_ptr()):
+        if b is not None and (mb is None or mb.data_ptr() != bp + r0 * bs):
             return False
-        r0 += r
+        r0 += mw.shape[0]
     return r0 == w.shape[0]
 
 

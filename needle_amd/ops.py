@@ -29,7 +29,10 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
 
 
 def _stream(dev: torch.device) -> int:
-    return torch.cuda.current_stream(dev).cuda_stream
+    """The raw handle of torch's current stream on dev (what current_stream(dev).cuda_stream
+    gives, without building a Stream object on every call)."""
+    idx = dev.index
+    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device() if idx is None else idx)
 
 
 def _require(cond: bool, msg: str, exc=ValueError) -> None:
@@ -38,28 +41,35 @@ def _require(cond: bool, msg: str, exc=ValueError) -> None:
 
 
 def _check_cache(kv_cache: torch.Tensor) -> None:
-    _require(kv_cache.dim() == 5 and kv_cache.shape[0] == 2,
-             f"kv_cache must be [2, num_blocks, num_kv_heads, block_size, head_dim], "
-             f"got {tuple(kv_cache.shape)}")
+    if kv_cache.dim() != 5 or kv_cache.shape[0] != 2:
+        raise ValueError("kv_cache must be [2, num_blocks, num_kv_heads, block_size, "
+                         f"head_dim], got {tuple(kv_cache.shape)}")
     _require(kv_cache.is_cuda, "kv_cache must be a GPU tensor")
     _require(kv_cache.is_contiguous(), "kv_cache must be contiguous")
-    _require(kv_cache.dtype in _DTYPES, f"unsupported kv_cache dtype {kv_cache.dtype}", TypeError)
+    if kv_cache.dtype not in _DTYPES:
+        raise TypeError(f"unsupported kv_cache dtype {kv_cache.dtype}")
 
 
 def _check_int32(name: str, t: torch.Tensor, dim: int, device) -> None:
-    _require(t.dtype == torch.int32, f"{name} must be int32, got {t.dtype}", TypeError)
-    _require(t.dim() == dim, f"{name} must have {dim} dims, got {t.dim()}")
-    _require(t.device == device, f"{name} must be on {device}, got {t.device}")
-    _require(t.stride(-1) == 1, f"{name} must be contiguous along its last dim")
+    # Messages are formatted only on failure: these checks run on every launch.
+    if t.dtype != torch.int32:
+        raise TypeError(f"{name} must be int32, got {t.dtype}")
+    if t.dim() != dim:
+        raise ValueError(f"{name} must have {dim} dims, got {t.dim()}")
+    if t.device != device:
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+    if t.stride(-1) != 1:
+        raise ValueError(f"{name} must be contiguous along its last dim")
 
 
 def _rows(name: str, x: torch.Tensor, n_heads: int, head_dim: int, device) -> int:
     """Token stride of a [T, n_heads, head_dim] tensor with contiguous inner rows."""
-    _require(x.dim() == 3 and x.shape[1] == n_heads and x.shape[2] == head_dim,
-             f"{name} must be [T, {n_heads}, {head_dim}], got {tuple(x.shape)}")
-    _require(x.device == device, f"{name} must be on {device}")
-    _require(x.stride(2) == 1 and x.stride(1) == head_dim,
-             f"{name} rows must be contiguous (strides {x.stride()})")
+    if x.dim() != 3 or x.shape[1] != n_heads or x.shape[2] != head_dim:
+        raise ValueError(f"{name} must be [T, {n_heads}, {head_dim}], got {tuple(x.shape)}")
+    if x.device != device:
+        raise ValueError(f"{name} must be on {device}")
+    if x.stride(2) != 1 or x.stride(1) != head_dim:
+        raise ValueError(f"{name} rows must be contiguous (strides {x.stride()})")
     return x.stride(0) if x.shape[0] > 1 else n_heads * head_dim
 
 
@@ -134,26 +144,30 @@ def rope_kv_append(q: Optional[torch.Tensor], k: torch.Tensor, v: torch.Tensor,
     dev = kv_cache.device
     _, num_blocks, hkv, bs, d = kv_cache.shape
     for name, x in (("q", q), ("k", k), ("v", v), ("cos", cos), ("sin", sin)):
-        _require(x is None or x.dtype == kv_cache.dtype, f"{name} dtype must match kv_cache",
-                 TypeError)
+        if x is not None and x.dtype != kv_cache.dtype:
+            raise TypeError(f"{name} dtype must match kv_cache")
     ks = _rows("k", k, hkv, d, dev)
     vs = _rows("v", v, hkv, d, dev)
     n_tok = k.shape[0]
     if q is not None:
-        _require(q.dim() == 3, f"q must be [T, H, {d}], got {tuple(q.shape)}")
+        if q.dim() != 3:
+            raise ValueError(f"q must be [T, H, {d}], got {tuple(q.shape)}")
         h = q.shape[1]
         qs = _rows("q", q, h, d, dev)
         _require(q.shape[0] == n_tok, "q/k/v token counts differ")
-        _require(h % hkv == 0, f"num_heads {h} not a multiple of num_kv_heads {hkv}")
+        if h % hkv:
+            raise ValueError(f"num_heads {h} not a multiple of num_kv_heads {hkv}")
     else:
         _require(out is None, "out is the rotated q: pass q with it")
         h, qs = hkv, 0
     _require(v.shape[0] == n_tok, "q/k/v token counts differ")
-    _require(d % 16 == 0, f"head_dim {d} must be a multiple of 16")
+    if d % 16:
+        raise ValueError(f"head_dim {d} must be a multiple of 16")
     for name, x in (("cos", cos), ("sin", sin)):
-        _require(x.dim() == 2 and x.shape[0] == n_tok and x.shape[1] == d,
-                 f"{name} must be [{n_tok}, {d}], got {tuple(x.shape)}")
-        _require(x.device == dev and x.stride(1) == 1, f"{name} rows must be contiguous on {dev}")
+        if x.dim() != 2 or x.shape[0] != n_tok or x.shape[1] != d:
+            raise ValueError(f"{name} must be [{n_tok}, {d}], got {tuple(x.shape)}")
+        if x.device != dev or x.stride(1) != 1:
+            raise ValueError(f"{name} rows must be contiguous on {dev}")
     _require(cos.stride(0) == sin.stride(0) or n_tok <= 1, "cos and sin token strides differ")
     cs = cos.stride(0) if n_tok > 1 else d
     _check_int32("block_table", block_table, 2, dev)
@@ -338,11 +352,12 @@ def varlen_prefill(q: torch.Tensor, kv_cache: torch.Tensor, block_table: torch.T
     cs = 0
     if cos is not None:
         for name, x in (("cos", cos), ("sin", sin)):
-            _require(x.dtype == q.dtype, f"{name} dtype must match q", TypeError)
-            _require(x.dim() == 2 and x.shape[0] == n_tok and x.shape[1] == head_dim,
-                     f"{name} must be [{n_tok}, {head_dim}], got {tuple(x.shape)}")
-            _require(x.device == dev and x.stride(1) == 1,
-                     f"{name} rows must be contiguous on {dev}")
+            if x.dtype != q.dtype:
+                raise TypeError(f"{name} dtype must match q")
+            if x.dim() != 2 or x.shape[0] != n_tok or x.shape[1] != head_dim:
+                raise ValueError(f"{name} must be [{n_tok}, {head_dim}], got {tuple(x.shape)}")
+            if x.device != dev or x.stride(1) != 1:
+                raise ValueError(f"{name} rows must be contiguous on {dev}")
         _require(cos.stride(0) == sin.stride(0) or n_tok <= 1, "cos and sin token strides differ")
         cs = cos.stride(0) if n_tok > 1 else head_dim
     if out is None:
@@ -428,14 +443,17 @@ def kv_block_copy(dst_pools, src_pools, src_ids: torch.Tensor, dst_ids: torch.Te
 
 def _row_stride(name: str, x: torch.Tensor, width: int, dtype, device) -> int:
     """Row stride of a [rows, width] tensor whose rows are contiguous and 16-byte aligned."""
-    _require(x.dim() == 2 and x.shape[1] == width, f"{name} must be [rows, {width}], "
-             f"got {tuple(x.shape)}")
-    _require(x.dtype == dtype, f"{name} must be {dtype}, got {x.dtype}", TypeError)
-    _require(x.device == device, f"{name} must be on {device}, got {x.device}")
-    _require(x.stride(1) == 1 or x.shape[1] == 1, f"{name} rows must be contiguous")
+    if x.dim() != 2 or x.shape[1] != width:
+        raise ValueError(f"{name} must be [rows, {width}], got {tuple(x.shape)}")
+    if x.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {x.dtype}")
+    if x.device != device:
+        raise ValueError(f"{name} must be on {device}, got {x.device}")
+    if x.stride(1) != 1 and x.shape[1] != 1:
+        raise ValueError(f"{name} rows must be contiguous")
     stride = x.stride(0) if x.shape[0] > 1 else width
-    _require(stride % 8 == 0 and x.data_ptr() % 16 == 0,
-             f"{name} rows must start 16-byte aligned (row stride {stride})")
+    if stride % 8 or x.data_ptr() % 16:
+        raise ValueError(f"{name} rows must start 16-byte aligned (row stride {stride})")
     return stride
 
 
@@ -450,18 +468,20 @@ def rms_norm(x: torch.Tensor, weight: torch.Tensor, eps: float,
     one dtype (bfloat16, float16 or float32), on one GPU.
     """
     _require(x.is_cuda, "x must be a GPU tensor")
-    _require(x.dtype in _DTYPES, f"unsupported dtype {x.dtype}", TypeError)
-    _require(x.dim() == 2, f"x must be [rows, hidden], got {tuple(x.shape)}")
+    if x.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {x.dtype}")
+    if x.dim() != 2:
+        raise ValueError(f"x must be [rows, hidden], got {tuple(x.shape)}")
     rows, hidden = x.shape
     stride = _row_stride("x", x, hidden, x.dtype, x.device)
-    _require(weight.shape == (hidden,) and weight.dtype == x.dtype and
-             weight.device == x.device and weight.is_contiguous(),
-             f"weight must be a contiguous [{hidden}] {x.dtype} tensor on {x.device}")
+    if (weight.shape != (hidden,) or weight.dtype != x.dtype or weight.device != x.device
+            or not weight.is_contiguous()):
+        raise ValueError(f"weight must be a contiguous [{hidden}] {x.dtype} tensor on {x.device}")
     out = torch.empty((rows, hidden), dtype=x.dtype, device=x.device)
     res_out = None
     if residual is not None:
-        _require(residual.shape == x.shape and residual.is_contiguous(),
-                 f"residual must be a contiguous {tuple(x.shape)} tensor")
+        if residual.shape != x.shape or not residual.is_contiguous():
+            raise ValueError(f"residual must be a contiguous {tuple(x.shape)} tensor")
         _row_stride("residual", residual, hidden, x.dtype, x.device)
         res_out = torch.empty_like(out)
     lib = _lib.load()
@@ -478,12 +498,15 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
     [rows, intermediate] with contiguous rows (e.g. the two halves of one fused gate/up
     projection output); returns a new [rows, intermediate] tensor."""
     _require(gate.is_cuda, "gate must be a GPU tensor")
-    _require(gate.dtype in _DTYPES, f"unsupported dtype {gate.dtype}", TypeError)
-    _require(gate.dim() == 2, f"gate must be [rows, intermediate], got {tuple(gate.shape)}")
+    if gate.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {gate.dtype}")
+    if gate.dim() != 2:
+        raise ValueError(f"gate must be [rows, intermediate], got {tuple(gate.shape)}")
     rows, inter = gate.shape
     gs = _row_stride("gate", gate, inter, gate.dtype, gate.device)
     us = _row_stride("up", up, inter, gate.dtype, gate.device)
-    _require(up.shape[0] == rows, f"up has {up.shape[0]} rows, gate {rows}")
+    if up.shape[0] != rows:
+        raise ValueError(f"up has {up.shape[0]} rows, gate {rows}")
     out = torch.empty((rows, inter), dtype=gate.dtype, device=gate.device)
     lib = _lib.load()
     rc = lib.ndl_silu_mul(out.data_ptr(), gate.data_ptr(), gs, up.data_ptr(), us, rows, inter,
@@ -499,15 +522,18 @@ def greedy_argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> t
     16-byte aligned rows; out: int32 or int64 [rows] on the same GPU (a new int64 tensor by
     default).  Graph-capturable."""
     _require(logits.is_cuda, "logits must be a GPU tensor")
-    _require(logits.dtype in _DTYPES, f"unsupported dtype {logits.dtype}", TypeError)
-    _require(logits.dim() == 2, f"logits must be [rows, vocab], got {tuple(logits.shape)}")
+    if logits.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {logits.dtype}")
+    if logits.dim() != 2:
+        raise ValueError(f"logits must be [rows, vocab], got {tuple(logits.shape)}")
     rows, vocab = logits.shape
     stride = _row_stride("logits", logits, vocab, logits.dtype, logits.device)
     if out is None:
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)
-    _require(out.dtype in (torch.int32, torch.int64) and out.shape == (rows,) and
-             out.is_contiguous() and out.device == logits.device,
-             f"out must be a contiguous int32 or int64 [{rows}] tensor on {logits.device}")
+    if (out.dtype not in (torch.int32, torch.int64) or out.shape != (rows,) or
+            not out.is_contiguous() or out.device != logits.device):
+        raise ValueError(f"out must be a contiguous int32 or int64 [{rows}] tensor on "
+                         f"{logits.device}")
     lib = _lib.load()
     nbytes = lib.ndl_greedy_argmax_workspace_bytes(rows, vocab) if rows > 0 else 0
     ws = torch.empty(nbytes, dtype=torch.uint8, device=logits.device) if nbytes else None

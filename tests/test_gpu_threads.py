@@ -80,3 +80,27 @@ def test_concurrent_threads_match_serial():
         assert torch.equal(pool.view(torch.int16), want_pool.view(torch.int16)), kind
         for o in outs:
             assert torch.equal(o.view(torch.int16), want.view(torch.int16)), kind
+
+
+def test_launch_stream_is_torchs_current_stream():
+    """Every entry point launches on the handle ops._stream gives: torch's current stream of
+    the calling thread, also inside a `with torch.cuda.stream(...)` block and on a thread of
+    its own."""
+    dev = torch.device(DEV)
+    assert ops._stream(dev) == torch.cuda.current_stream(dev).cuda_stream
+    assert ops._stream(torch.device("cuda")) == torch.cuda.current_stream().cuda_stream
+    side = torch.cuda.Stream()
+    with torch.cuda.stream(side):
+        assert ops._stream(dev) == side.cuda_stream
+    assert ops._stream(dev) == torch.cuda.current_stream(dev).cuda_stream
+    seen = []
+
+    def worker():
+        own = torch.cuda.Stream()
+        with torch.cuda.stream(own):
+            seen.append(ops._stream(dev) == own.cuda_stream)
+
+    t = threading.Thread(target=worker)
+    t.start()
+    t.join(timeout=60)
+    assert seen == [True]
