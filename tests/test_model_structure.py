@@ -91,3 +91,49 @@ def test_residual_stream_matches_the_reference_layer(model_type, dtype):
     for x, y in zip(new.kv_caches, ref.kv_caches):
         assert torch.equal(x, y)
     assert forwards >= 6
+
+
+@pytest.mark.parametrize("bias", [True, False])
+def test_fused_projection_check(bias):
+    """fused_outputs uses the one GEMM over the fused weight only while every layer's weight
+    (and bias) is still the view fuse_linears made at that layer's own rows; otherwise each
+    layer runs its own GEMM.  Two equal-sized layers with their parameters swapped stay
+    views of the fused tensor, at each other's rows: the check must see that too."""
+    from torch import nn
+    from needle_amd.layers.attention import _still_fused, fuse_linears, fused_outputs
+
+    def layers():
+        torch.manual_seed(5)
+        mods = [nn.Linear(32, n, bias=bias, dtype=torch.float64) for n in (48, 16, 16)]
+        return mods, fuse_linears(*mods)
+
+    x = torch.randn(5, 32, dtype=torch.float64)
+    mods, fused = layers()
+    assert _still_fused(fused, mods)
+    want = [m(x) for m in mods]
+    for got, ref in zip(fused_outputs(fused, mods, x), want):
+        torch.testing.assert_close(got, ref, rtol=1e-12, atol=1e-12)
+
+    mods, fused = layers()                     # k and v parameters swapped: views, wrong rows
+    mods[1].weight, mods[2].weight = mods[2].weight, mods[1].weight
+    if bias:
+        mods[1].bias, mods[2].bias = mods[2].bias, mods[1].bias
+    assert not _still_fused(fused, mods)
+    for got, m in zip(fused_outputs(fused, mods, x), mods):
+        assert torch.equal(got, m(x))
+
+    mods, fused = layers()                     # a replaced weight (a load that assigns)
+    mods[0].weight = nn.Parameter(mods[0].weight.detach().clone())
+    assert not _still_fused(fused, mods)
+
+    mods, fused = layers()                     # a moved layer gets storage of its own
+    mods[2].to(torch.float32)
+    assert not _still_fused(fused, mods)
+
+    if bias:
+        mods, fused = layers()                 # only a bias replaced
+        mods[2].bias = nn.Parameter(mods[2].bias.detach().clone())
+        assert not _still_fused(fused, mods)
+        mods, fused = layers()                 # a bias dropped
+        mods[1].bias = None
+        assert not _still_fused(fused, mods)
