@@ -28,11 +28,16 @@ def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
     return None if t is None else t.data_ptr()
 
 
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def _stream(dev: torch.device) -> int:
     """The raw handle of torch's current stream on dev (what current_stream(dev).cuda_stream
-    gives, without building a Stream object on every call)."""
+    gives, without building a Stream object on every call where torch exposes the handle)."""
+    if _raw_stream is None:
+        return torch.cuda.current_stream(dev).cuda_stream
     idx = dev.index
-    return torch._C._cuda_getCurrentRawStream(torch.cuda.current_device() if idx is None else idx)
+    return _raw_stream(torch.cuda.current_device() if idx is None else idx)
 
 
 def _require(cond: bool, msg: str, exc=ValueError) -> None:
