@@ -523,15 +523,24 @@ def silu_mul(gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
 def greedy_argmax(logits: torch.Tensor, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The index of each row's maximum, in torch's argmax order (needle/model/sampler.py:
     27-28, for the whole batch: one or two launches, the slices' partials in a workspace
-    allocated here, from the graph's pool under capture).  logits: [rows, vocab] with contiguous,
-    16-byte aligned rows; out: int32 or int64 [rows] on the same GPU (a new int64 tensor by
-    default).  Graph-capturable."""
+    allocated here, from the graph's pool under capture).  logits: [rows, vocab]; the kernel
+    reads contiguous rows that start 16-byte aligned, and other rows (a vocabulary that is not
+    a multiple of 8 elements wide, a column slice, a transposed view) are first copied into
+    such a buffer on the GPU.  out: int32 or int64 [rows] on the same GPU (a new int64 tensor
+    by default).  Graph-capturable."""
     _require(logits.is_cuda, "logits must be a GPU tensor")
     if logits.dtype not in _DTYPES:
         raise TypeError(f"unsupported dtype {logits.dtype}")
     if logits.dim() != 2:
         raise ValueError(f"logits must be [rows, vocab], got {tuple(logits.shape)}")
     rows, vocab = logits.shape
+    if rows > 0 and vocab > 0:
+        st = logits.stride(0) if rows > 1 else vocab
+        if (logits.stride(1) != 1 and vocab > 1) or st % 8 or logits.data_ptr() % 16:
+            padded = torch.empty((rows, (vocab + 7) // 8 * 8), dtype=logits.dtype,
+                                 device=logits.device)
+            padded[:, :vocab].copy_(logits)
+            logits = padded[:, :vocab]
     stride = _row_stride("logits", logits, vocab, logits.dtype, logits.device)
     if out is None:
         out = torch.empty(rows, dtype=torch.int64, device=logits.device)

@@ -4,7 +4,8 @@ Reference: needle/model/sampler.py:27-28 (int(logit.argmax()) per greedy row).  
 must return torch's index exactly: the first of equal maxima, a NaN above every number (the
 first NaN), -0 equal to +0.  Cases: random rows of the real vocabulary (151,936), rows drawn
 from a handful of values (ties everywhere, the common case of flat bf16 logits), NaN and
--inf rows, a vocabulary that is not a multiple of 8 read through a wider row stride, every
+-inf rows, a vocabulary that is not a multiple of 8 read through a wider row stride, rows
+that need an aligned copy first (an odd vocabulary, a shifted slice, a transposed view), every
 dtype, int32 and int64 outputs, rows scanned in one slice or several (ties across a slice
 edge), the workspace check, and the launches recorded in a HIP graph and replayed with eager
 work in between.
@@ -83,6 +84,25 @@ def test_argmax_strided_rows_and_tail():
     assert got[4].item() == 1001
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_argmax_unaligned_rows_are_copied_aligned(dtype):
+    """Rows the kernel cannot read in place (a contiguous vocabulary of 50,257, not a multiple
+    of 8; a column slice starting one element in; a transposed view) go through an aligned
+    copy and still give torch's index."""
+    g = torch.Generator().manual_seed(17)
+    odd = (torch.randn(37, 50257, generator=g) * 3).to(dtype).to(DEV)
+    odd[5, 50256] = 1000.0                                    # the last element of a row
+    got = ops.greedy_argmax(odd)
+    assert torch.equal(got.cpu(), _want(odd)) and got[5].item() == 50256
+    base = (torch.randn(6, 1025, generator=g) * 3).to(dtype).to(DEV)
+    shifted = base[:, 1:]                                     # data_ptr 2 or 4 bytes in
+    assert torch.equal(ops.greedy_argmax(shifted).cpu(), _want(shifted))
+    cols = (torch.randn(300, 7, generator=g) * 3).to(dtype).to(DEV).t()   # [7, 300], stride (1, 7)
+    out = torch.empty(7, dtype=torch.int32, device=DEV)
+    ops.greedy_argmax(cols, out=out)
+    assert torch.equal(out.cpu().long(), _want(cols))
+
+
 def test_argmax_in_a_graph():
     g = torch.Generator().manual_seed(3)
     logits = torch.randn(32, 151936, generator=g).to(torch.bfloat16).to(DEV)
@@ -103,9 +123,10 @@ def test_argmax_in_a_graph():
 
 def test_argmax_rejects_bad_arguments():
     from needle_amd._lib import NeedleAmdError
-    logits = torch.zeros(4, 100, dtype=torch.bfloat16, device=DEV)
-    with pytest.raises((ValueError, NeedleAmdError)):          # row stride not a multiple of 8
-        ops.greedy_argmax(logits)
+    with pytest.raises((ValueError, NeedleAmdError)):          # not [rows, vocab]
+        ops.greedy_argmax(torch.zeros(2, 4, 104, dtype=torch.bfloat16, device=DEV))
+    with pytest.raises(TypeError):
+        ops.greedy_argmax(torch.zeros(4, 104, dtype=torch.int32, device=DEV))
     with pytest.raises(ValueError):
         ops.greedy_argmax(torch.zeros(4, 104, dtype=torch.bfloat16, device=DEV),
                           out=torch.zeros(3, dtype=torch.int64, device=DEV))
