@@ -1,7 +1,8 @@
 """The drop-in Attention layer against the reference's Attention.forward (oracle).
 
-One Qwen2-0.5B-shaped layer (qkv bias, 14/2 heads, head_dim 64) and one
-Llama-3-8B-shaped layer: a prefill of three prompts, then two decode steps,
+One Qwen2-0.5B-shaped layer (qkv bias, 14/2 heads, head_dim 64), one Llama-3-8B-shaped
+layer and one with Qwen2-7B's heads (28/4, head_dim 128, qkv bias): a prefill of three
+prompts, then two decode steps,
 with the same weights on the GPU layer and on the CPU oracle.  Outputs agree
 to the bf16 parity tolerance |gpu - ref| <= 2e-2 + 1e-2 |ref|.  The pools are
 compared to the same tolerance after every call (not bit for bit) because the k/v projections run through different
@@ -29,12 +30,16 @@ def _close(got, want):
     assert np.isfinite(got).all() and excess.max() <= 0, float(np.abs(got - want).max())
 
 
-@pytest.mark.parametrize("cfg,bias", [
-    (ModelConfig(**QWEN2_0_5B), True),
+@pytest.mark.parametrize("cfg,bias,lens", [
+    (ModelConfig(**QWEN2_0_5B), True, [5, 33, 17]),
     (ModelConfig(hidden_size=4096, num_attention_heads=32, num_key_value_heads=8,
-                 rope_theta=500000.0, max_position_embeddings=8192), False)])
+                 rope_theta=500000.0, max_position_embeddings=8192), False, [5, 33, 17]),
+    # Qwen2-7B heads (28 / 4, head_dim 128): a group of 7, so a prefill workgroup's eight
+    # jobs span two 32-row subtiles; prompts of several subtiles each
+    (ModelConfig(hidden_size=3584, num_attention_heads=28, num_key_value_heads=4,
+                 rope_theta=1e6, max_position_embeddings=4096), True, [300, 129, 70])])
 @torch.no_grad()  # the runner calls the model under no_grad (runner.py:143, 151)
-def test_prefill_then_decode_matches_reference(cfg, bias):
+def test_prefill_then_decode_matches_reference(cfg, bias, lens):
     torch.manual_seed(0)
     layer = Attention(cfg, 0, qkv_bias=bias)
     for p in layer.parameters():
@@ -45,7 +50,6 @@ def test_prefill_then_decode_matches_reference(cfg, bias):
     rope = RotaryEmbedding(cfg.head_dim, 4096, cfg.rope_theta).to(torch.bfloat16)
 
     hkv, d, bs = cfg.num_key_value_heads, cfg.head_dim, 16
-    lens = [5, 33, 17]
     steps = 2
     blocks = [(n + steps + bs - 1) // bs for n in lens]
     nb = sum(blocks) + 4
